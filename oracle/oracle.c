@@ -1,0 +1,481 @@
+/*
+ * CPU oracle for the rLLM paged-attention path — TEST INFRASTRUCTURE ONLY.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+ * this code, always as the checker or the CPU baseline, never as the product.
+ * See oracle.h for the reference file:line each function restates.
+ */
+#define _GNU_SOURCE
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ------------------------------------------------------------------ */
+/* 16-bit float conversions                                            */
+/* ------------------------------------------------------------------ */
+
+float orc_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u); /* quiet NaN */
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0) {
+        /* zero or subnormal: m * 2^-24, exact in fp32 */
+        float v = (float)m * 0x1p-24f;
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t u = f2u(f);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7e00u;      /* NaN */
+    if (a >= 0x477ff000u) return sign | 0x7c00u;     /* >= 65520 rounds to inf */
+    if (a < 0x38800000u) {                            /* below 2^-14: f16 subnormal */
+        if (a < 0x33000000u) return sign;             /* <= 2^-25 rounds to zero */
+        uint32_t e = a >> 23;
+        uint32_t m = (a & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - e;                    /* value / 2^-24 = m >> shift */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return sign | (uint16_t)q;
+    }
+    uint32_t v = (a >> 13) - (112u << 10);
+    uint32_t rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (v & 1u))) v++;
+    return sign | (uint16_t)v;
+}
+
+/* ------------------------------------------------------------------ */
+/* FP8 codecs (cache_ops.cu:13-128)                                    */
+/* ------------------------------------------------------------------ */
+
+uint8_t orc_fp8_e4m3_encode_reftext(float x) {
+    if (isnan(x)) return 0x7F;
+    uint32_t u = f2u(x);
+    uint32_t sign = (u >> 31) & 1u;
+    uint32_t exp = (u >> 23) & 0xffu;
+    uint32_t mant = u & 0x7fffffu;
+    if (exp == 0) return (uint8_t)(sign << 7);
+    if (exp == 255) return (uint8_t)((sign << 7) | 0x7E);
+    int ne = (int)exp - 127 + 7;
+    if (ne <= 0) return (uint8_t)(sign << 7);
+    if (ne >= 16) return (uint8_t)((sign << 7) | 0x7E);
+    return (uint8_t)((sign << 7) | ((uint32_t)ne << 3) | (mant >> 20));
+}
+
+uint8_t orc_fp8_e4m3_encode(float x) {
+    uint8_t b = orc_fp8_e4m3_encode_reftext(x);
+    /* deliberate deviation: [480, 512) truncates onto the NaN code; saturate */
+    if (!isnan(x) && (b & 0x7F) == 0x7F) b = (uint8_t)((b & 0x80) | 0x7E);
+    return b;
+}
+
+float orc_fp8_e4m3_decode(uint8_t b) {
+    uint32_t sign = (b >> 7) & 1u, e = (b >> 3) & 0xfu, m = b & 7u;
+    float v;
+    if (e == 0) v = (float)m * 0x1p-9f;
+    else if (e == 15 && m == 7) return NAN;
+    else v = ldexpf(1.0f + (float)m * 0.125f, (int)e - 7);
+    return sign ? -v : v;
+}
+
+float orc_fp8_e4m3_decode_reftext(uint8_t b) {
+    uint32_t sign = (b >> 7) & 1u, e = (b >> 3) & 0xfu, m = b & 7u;
+    if (e == 0) {
+        float v = (float)m * 0.0078125f;
+        return sign ? -v : v;
+    }
+    if (e == 15 && m == 7) return NAN;
+    float v = ldexpf(1.0f + (float)m * 0.125f, (int)e - 7);
+    return sign ? -v : v;
+}
+
+uint8_t orc_fp8_e5m2_encode(float x) {
+    if (isnan(x)) return 0x7F;
+    uint32_t u = f2u(x);
+    uint32_t sign = (u >> 31) & 1u;
+    uint32_t exp = (u >> 23) & 0xffu;
+    uint32_t mant = u & 0x7fffffu;
+    if (exp == 0) return (uint8_t)(sign << 7);
+    if (exp == 255) return (uint8_t)((sign << 7) | 0x7B);
+    int ne = (int)exp - 127 + 15;
+    if (ne <= 0) return (uint8_t)(sign << 7);
+    if (ne >= 31) return (uint8_t)((sign << 7) | 0x7B);
+    return (uint8_t)((sign << 7) | ((uint32_t)ne << 2) | (mant >> 21));
+}
+
+float orc_fp8_e5m2_decode(uint8_t b) {
+    uint32_t sign = (b >> 7) & 1u, e = (b >> 2) & 0x1fu, m = b & 3u;
+    float v;
+    if (e == 0) v = (float)m * 0x1p-16f;
+    else if (e == 31) v = (m == 0) ? INFINITY : NAN;
+    else v = ldexpf(1.0f + (float)m * 0.25f, (int)e - 15);
+    return sign ? -v : v;
+}
+
+static inline float decode_elem(const void *base, int kind, int64_t i) {
+    switch (kind) {
+    case ORC_F16: return orc_f16_to_f32(((const uint16_t *)base)[i]);
+    case ORC_BF16: return orc_bf16_to_f32(((const uint16_t *)base)[i]);
+    case ORC_FP8_E4M3: return orc_fp8_e4m3_decode(((const uint8_t *)base)[i]);
+    default: return orc_fp8_e5m2_decode(((const uint8_t *)base)[i]);
+    }
+}
+
+void orc_decode_array(const void *src, int kind, int64_t n, float *dst) {
+    for (int64_t i = 0; i < n; i++) dst[i] = decode_elem(src, kind, i);
+}
+
+void orc_encode_array(const float *src, int kind, int64_t n, void *dst) {
+    for (int64_t i = 0; i < n; i++) {
+        switch (kind) {
+        case ORC_F16: ((uint16_t *)dst)[i] = orc_f32_to_f16(src[i]); break;
+        case ORC_BF16: ((uint16_t *)dst)[i] = orc_f32_to_bf16(src[i]); break;
+        case ORC_FP8_E4M3: ((uint8_t *)dst)[i] = orc_fp8_e4m3_encode(src[i]); break;
+        default: ((uint8_t *)dst)[i] = orc_fp8_e5m2_encode(src[i]); break;
+        }
+    }
+}
+
+/* ---- exhaustive encoder checks --------------------------------------- */
+
+typedef struct {
+    uint64_t lo, hi;
+    int e5m2;
+    int64_t bad;
+    uint32_t first_bad;
+} exh_job;
+
+/* Round-toward-zero characterisation, written against the decoder only. */
+static int e4m3_ok(uint32_t u) {
+    float x = u2f(u);
+    uint8_t b = orc_fp8_e4m3_encode(x);
+    if (isnan(x)) return b == 0x7F;
+    if ((b >> 7) != (u >> 31)) return 0;
+    float a = fabsf(x);
+    uint8_t mag = b & 0x7F;
+    if (a < 0x1p-6f) return mag == 0;
+    if (a >= 448.0f) return mag == 0x7E;
+    if (mag < 0x08 || mag > 0x7E) return 0;
+    float lo = orc_fp8_e4m3_decode(mag);
+    float hi = orc_fp8_e4m3_decode((uint8_t)(mag + 1));
+    if (mag + 1 == 0x7F) hi = 480.0f; /* next magnitude the format would have */
+    return lo <= a && a < hi;
+}
+
+static int e5m2_ok(uint32_t u) {
+    float x = u2f(u);
+    uint8_t b = orc_fp8_e5m2_encode(x);
+    if (isnan(x)) return b == 0x7F;
+    if ((b >> 7) != (u >> 31)) return 0;
+    float a = fabsf(x);
+    uint8_t mag = b & 0x7F;
+    if (a < 0x1p-14f) return mag == 0;
+    if (a >= 57344.0f) return mag == 0x7B;
+    if (mag < 0x04 || mag > 0x7B) return 0;
+    float lo = orc_fp8_e5m2_decode(mag);
+    float hi = (mag == 0x7B) ? 65536.0f : orc_fp8_e5m2_decode((uint8_t)(mag + 1));
+    return lo <= a && a < hi;
+}
+
+static void *exh_worker(void *p) {
+    exh_job *j = (exh_job *)p;
+    for (uint64_t v = j->lo; v < j->hi; v++) {
+        uint32_t u = (uint32_t)v;
+        int ok = j->e5m2 ? e5m2_ok(u) : e4m3_ok(u);
+        if (!ok) {
+            if (j->bad == 0) j->first_bad = u;
+            j->bad++;
+        }
+    }
+    return NULL;
+}
+
+static int64_t run_exhaustive(int e5m2, int nthreads, uint32_t *first_bad) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    exh_job jobs[256];
+    uint64_t total = 1ull << 32, step = (total + nthreads - 1) / nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        jobs[t].lo = step * t;
+        jobs[t].hi = step * (t + 1) < total ? step * (t + 1) : total;
+        jobs[t].e5m2 = e5m2;
+        jobs[t].bad = 0;
+        jobs[t].first_bad = 0;
+        pthread_create(&th[t], NULL, exh_worker, &jobs[t]);
+    }
+    int64_t bad = 0;
+    int have = 0;
+    for (int t = 0; t < nthreads; t++) {
+        pthread_join(th[t], NULL);
+        if (jobs[t].bad && !have) { have = 1; if (first_bad) *first_bad = jobs[t].first_bad; }
+        bad += jobs[t].bad;
+    }
+    return bad;
+}
+
+int64_t orc_fp8_e4m3_exhaustive(int nthreads, uint32_t *first_bad) {
+    return run_exhaustive(0, nthreads, first_bad);
+}
+
+int64_t orc_fp8_e5m2_exhaustive(int nthreads, uint32_t *first_bad) {
+    return run_exhaustive(1, nthreads, first_bad);
+}
+
+/* ------------------------------------------------------------------ */
+/* slot mapping (model_runner.rs:806-826)                              */
+/* ------------------------------------------------------------------ */
+
+void orc_slot_mapping(const uint32_t *positions, int64_t n, const uint32_t *block_table,
+                      int64_t bt_len, int64_t block_size, int64_t *out) {
+    for (int64_t i = 0; i < n; i++) {
+        if (block_size <= 0 || block_size > 0xffffffffll) { out[i] = -1; continue; }
+        uint32_t bs = (uint32_t)block_size;
+        uint32_t bi = positions[i] / bs, off = positions[i] % bs;
+        out[i] = ((int64_t)bi < bt_len) ? (int64_t)block_table[bi] * (int64_t)bs + off : -1;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* reshape_and_cache (cache_ops.cu:161-200, 322-364)                   */
+/* ------------------------------------------------------------------ */
+
+void orc_cache_write(void *key_cache, void *value_cache, const void *new_key,
+                     const void *new_value, const int64_t *slot_mapping, int64_t num_tokens,
+                     int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                     int64_t num_blocks, int in_kind, int cache_kind, float k_scale,
+                     float v_scale) {
+    for (int64_t t = 0; t < num_tokens; t++) {
+        int64_t slot = slot_mapping[t];
+        if (slot < 0) continue;
+        int64_t blk = slot / block_size, off = slot % block_size;
+        if (blk >= num_blocks) continue;
+        for (int64_t h = 0; h < num_kv_heads; h++) {
+            for (int64_t d = 0; d < head_dim; d++) {
+                int64_t dst = ((blk * num_kv_heads + h) * head_dim + d) * block_size + off;
+                int64_t src = (t * num_kv_heads + h) * head_dim + d;
+                if (cache_kind == ORC_F16 || cache_kind == ORC_BF16) {
+                    ((uint16_t *)key_cache)[dst] = ((const uint16_t *)new_key)[src];
+                    ((uint16_t *)value_cache)[dst] = ((const uint16_t *)new_value)[src];
+                } else {
+                    float kx = decode_elem(new_key, in_kind, src) / k_scale;
+                    float vx = decode_elem(new_value, in_kind, src) / v_scale;
+                    uint8_t kb = cache_kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode(kx)
+                                                            : orc_fp8_e5m2_encode(kx);
+                    uint8_t vb = cache_kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode(vx)
+                                                            : orc_fp8_e5m2_encode(vx);
+                    ((uint8_t *)key_cache)[dst] = kb;
+                    ((uint8_t *)value_cache)[dst] = vb;
+                }
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* attention                                                            */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    float *out;
+    const void *q;
+    int q_kind;
+    const void *kc, *vc;
+    int cache_kind;
+    const int32_t *bt, *seq_lens, *qsl;
+    int64_t num_seqs, num_tokens, hq, hkv, d, bs, maxb;
+    float scale, k_scale, v_scale;
+    int precision;
+    int prefill;
+    atomic_long next;
+} attn_job;
+
+/* Gather the K and V rows a (sequence, kv head) pair can attend to into
+ * contiguous [n][D] arrays, in logical token order, skipping tokens whose
+ * block-table entry is negative (paged_attention.cu:129-136).  pos[] keeps the
+ * logical position of each gathered token for causal masking. */
+static int64_t gather(const attn_job *j, int64_t s, int64_t h, int64_t ctx, float *K, float *V,
+                      int64_t *pos) {
+    int64_t nblk = (ctx + j->bs - 1) / j->bs;
+    if (nblk > j->maxb) nblk = j->maxb;
+    int64_t n = 0;
+    for (int64_t b = 0; b < nblk; b++) {
+        int64_t pb = j->bt[s * j->maxb + b];
+        if (pb < 0) continue;
+        for (int64_t off = 0; off < j->bs; off++) {
+            int64_t t = b * j->bs + off;
+            if (t >= ctx) break;
+            for (int64_t dd = 0; dd < j->d; dd++) {
+                int64_t idx = ((pb * j->hkv + h) * j->d + dd) * j->bs + off;
+                K[n * j->d + dd] = decode_elem(j->kc, j->cache_kind, idx) * j->k_scale;
+                V[n * j->d + dd] = decode_elem(j->vc, j->cache_kind, idx) * j->v_scale;
+            }
+            pos[n++] = t;
+        }
+    }
+    return n;
+}
+
+/* softmax(scale * q.K^T) V over the first `lim` gathered rows whose position
+ * is <= max_pos (SDPA of layers.rs:325-340, done in fp32 or fp64). */
+static void attend_f32(const float *q, const float *K, const float *V, const int64_t *pos,
+                       int64_t n, int64_t max_pos, int64_t D, float scale, float *sc,
+                       float *out) {
+    float m = -INFINITY;
+    int64_t cnt = 0;
+    for (int64_t t = 0; t < n && pos[t] <= max_pos; t++) {
+        float acc = 0.0f;
+        for (int64_t dd = 0; dd < D; dd++) acc += q[dd] * K[t * D + dd];
+        sc[t] = acc * scale;
+        if (sc[t] > m) m = sc[t];
+        cnt = t + 1;
+    }
+    for (int64_t dd = 0; dd < D; dd++) out[dd] = 0.0f;
+    if (cnt == 0) return;
+    float l = 0.0f;
+    for (int64_t t = 0; t < cnt; t++) {
+        float p = expf(sc[t] - m);
+        l += p;
+        for (int64_t dd = 0; dd < D; dd++) out[dd] += p * V[t * D + dd];
+    }
+    for (int64_t dd = 0; dd < D; dd++) out[dd] /= l;
+}
+
+static void attend_f64(const float *q, const float *K, const float *V, const int64_t *pos,
+                       int64_t n, int64_t max_pos, int64_t D, float scale, double *sc,
+                       double *acc_o, float *out) {
+    double m = -INFINITY;
+    int64_t cnt = 0;
+    for (int64_t t = 0; t < n && pos[t] <= max_pos; t++) {
+        double acc = 0.0;
+        for (int64_t dd = 0; dd < D; dd++) acc += (double)q[dd] * (double)K[t * D + dd];
+        sc[t] = acc * (double)scale;
+        if (sc[t] > m) m = sc[t];
+        cnt = t + 1;
+    }
+    for (int64_t dd = 0; dd < D; dd++) { acc_o[dd] = 0.0; out[dd] = 0.0f; }
+    if (cnt == 0) return;
+    double l = 0.0;
+    for (int64_t t = 0; t < cnt; t++) {
+        double p = exp(sc[t] - m);
+        l += p;
+        for (int64_t dd = 0; dd < D; dd++) acc_o[dd] += p * (double)V[t * D + dd];
+    }
+    for (int64_t dd = 0; dd < D; dd++) out[dd] = (float)(acc_o[dd] / l);
+}
+
+static void *attn_worker(void *p) {
+    attn_job *j = (attn_job *)p;
+    int64_t D = j->d, G = j->hq / j->hkv;
+    int64_t cap = j->maxb * j->bs;
+    float *K = (float *)malloc(sizeof(float) * (size_t)(cap * D + 1));
+    float *V = (float *)malloc(sizeof(float) * (size_t)(cap * D + 1));
+    int64_t *pos = (int64_t *)malloc(sizeof(int64_t) * (size_t)(cap + 1));
+    float *sc = (float *)malloc(sizeof(float) * (size_t)(cap + 1));
+    double *scd = (double *)malloc(sizeof(double) * (size_t)(cap + 1));
+    double *acc = (double *)malloc(sizeof(double) * (size_t)D);
+    float *qf = (float *)malloc(sizeof(float) * (size_t)D);
+    int64_t units = j->num_seqs * j->hkv;
+    for (;;) {
+        int64_t u = atomic_fetch_add(&j->next, 1);
+        if (u >= units) break;
+        int64_t s = u / j->hkv, h = u % j->hkv;
+        int64_t ctx = j->seq_lens[s];
+        if (ctx < 0) ctx = 0;
+        int64_t n = gather(j, s, h, ctx, K, V, pos);
+        int64_t t0 = 0, t1 = 1; /* query tokens of this sequence */
+        if (j->prefill) { t0 = j->qsl[s]; t1 = j->qsl[s + 1]; }
+        for (int64_t tok = t0; tok < t1; tok++) {
+            int64_t row = j->prefill ? tok : s;
+            int64_t max_pos = j->prefill ? ctx - (t1 - t0) + (tok - t0) : ctx - 1;
+            for (int64_t g = 0; g < G; g++) {
+                /* every q head whose kv head (qh * Hkv / Hq, attention.rs:40-42) is h */
+                int64_t qh = h * G + g;
+                int64_t base = (row * j->hq + qh) * D;
+                for (int64_t dd = 0; dd < D; dd++) qf[dd] = decode_elem(j->q, j->q_kind, base + dd);
+                float *o = j->out + base;
+                if (j->precision == 0) attend_f32(qf, K, V, pos, n, max_pos, D, j->scale, sc, o);
+                else attend_f64(qf, K, V, pos, n, max_pos, D, j->scale, scd, acc, o);
+            }
+        }
+    }
+    free(K); free(V); free(pos); free(sc); free(scd); free(acc); free(qf);
+    return NULL;
+}
+
+static void run_attn(attn_job *j, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 512) nthreads = 512;
+    atomic_store(&j->next, 0);
+    if (nthreads == 1) { attn_worker(j); return; }
+    pthread_t th[512];
+    for (int t = 0; t < nthreads; t++) pthread_create(&th[t], NULL, attn_worker, j);
+    for (int t = 0; t < nthreads; t++) pthread_join(th[t], NULL);
+}
+
+void orc_paged_attention_decode(float *out, const void *q, int q_kind, const void *key_cache,
+                                const void *value_cache, int cache_kind,
+                                const int32_t *block_tables, const int32_t *seq_lens,
+                                int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
+                                int64_t head_dim, int64_t block_size,
+                                int64_t max_num_blocks_per_seq, float scale, float k_scale,
+                                float v_scale, int precision, int nthreads) {
+    if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return;
+    attn_job j = {
+        .out = out, .q = q, .q_kind = q_kind, .kc = key_cache, .vc = value_cache,
+        .cache_kind = cache_kind, .bt = block_tables, .seq_lens = seq_lens, .qsl = NULL,
+        .num_seqs = num_seqs, .num_tokens = num_seqs, .hq = num_q_heads, .hkv = num_kv_heads,
+        .d = head_dim, .bs = block_size, .maxb = max_num_blocks_per_seq, .scale = scale,
+        .k_scale = k_scale, .v_scale = v_scale, .precision = precision, .prefill = 0,
+    };
+    run_attn(&j, nthreads);
+}
+
+void orc_paged_attention_prefill(float *out, const void *q, int q_kind, const void *key_cache,
+                                 const void *value_cache, int cache_kind,
+                                 const int32_t *block_tables, const int32_t *seq_lens,
+                                 const int32_t *query_start_loc, int64_t num_seqs,
+                                 int64_t num_tokens, int64_t num_q_heads, int64_t num_kv_heads,
+                                 int64_t head_dim, int64_t block_size,
+                                 int64_t max_num_blocks_per_seq, float scale, float k_scale,
+                                 float v_scale, int precision, int nthreads) {
+    if (num_seqs <= 0 || num_tokens <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads)
+        return;
+    attn_job j = {
+        .out = out, .q = q, .q_kind = q_kind, .kc = key_cache, .vc = value_cache,
+        .cache_kind = cache_kind, .bt = block_tables, .seq_lens = seq_lens,
+        .qsl = query_start_loc, .num_seqs = num_seqs, .num_tokens = num_tokens,
+        .hq = num_q_heads, .hkv = num_kv_heads, .d = head_dim, .bs = block_size,
+        .maxb = max_num_blocks_per_seq, .scale = scale, .k_scale = k_scale,
+        .v_scale = v_scale, .precision = precision, .prefill = 1,
+    };
+    run_attn(&j, nthreads);
+}
+
+int orc_hardware_threads(void) {
+    long n = sysconf(_SC_NPROCESSORS_ONLN);
+    return n > 0 ? (int)n : 1;
+}

@@ -1,0 +1,168 @@
+"""torch-tensor front end of the C ABI, used by the tests and the benchmark.
+
+torch supplies device memory and the current HIP stream; every computation is
+one of the library's gfx950 kernels.  Shapes, dtypes, devices and (optionally)
+block-table bounds are checked on the host before any launch, so a kernel
+never sees operands that disagree with its grid.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ._lib import DTYPE_BF16, DTYPE_F16, DTYPE_FP8_E4M3, DTYPE_FP8_E5M2, call
+
+_TORCH_16 = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+
+
+def _stream(stream: Optional[torch.cuda.Stream]) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+def _kv_code(cache: torch.Tensor, kv_dtype: Optional[int]) -> int:
+    if cache.dtype in _TORCH_16:
+        code = _TORCH_16[cache.dtype]
+        if kv_dtype is not None and kv_dtype != code:
+            raise ValueError("kv_dtype disagrees with the cache tensor dtype")
+        return code
+    if cache.dtype == torch.uint8:
+        if kv_dtype not in (DTYPE_FP8_E4M3, DTYPE_FP8_E5M2):
+            raise ValueError("a uint8 cache needs kv_dtype FP8_E4M3 or FP8_E5M2")
+        return kv_dtype
+    raise TypeError(f"unsupported cache dtype {cache.dtype}")
+
+
+def _check_common(q, k_cache, v_cache, block_tables, seq_lens, nseq_dim0):
+    dev = q.device
+    if dev.type != "cuda":
+        raise ValueError("tensors must live on a GPU")
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("block_tables", block_tables),
+                    ("seq_lens", seq_lens)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, q on {dev}")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if not q.is_contiguous():
+        raise ValueError("q must be contiguous")
+    if q.dim() != 3 or k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("q [*, Hq, D] and caches [nb, Hkv, D, bs] of equal shape required")
+    if k_cache.dtype != v_cache.dtype:
+        raise ValueError("k_cache and v_cache dtypes differ")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise TypeError("block_tables and seq_lens must be int32")
+    if block_tables.dim() != 2 or block_tables.shape[0] != nseq_dim0 or seq_lens.shape != (nseq_dim0,):
+        raise ValueError("block_tables [num_seqs, max_blocks] and seq_lens [num_seqs] required")
+    if q.shape[2] != k_cache.shape[2]:
+        raise ValueError("head_dim of q and caches differ")
+    if q.dtype not in _TORCH_16:
+        raise TypeError("q must be float16 or bfloat16")
+
+
+def validate_tables(block_tables: torch.Tensor, seq_lens: torch.Tensor, num_blocks: int,
+                    block_size: int) -> None:
+    """Every table entry a sequence's context reaches must be < num_blocks
+    (negative entries are skipped by the kernels)."""
+    bt = block_tables.detach().cpu()
+    sl = seq_lens.detach().cpu()
+    maxb = bt.shape[1]
+    for s in range(bt.shape[0]):
+        n = min((max(int(sl[s]), 0) + block_size - 1) // block_size, maxb)
+        if n and int(bt[s, :n].max()) >= num_blocks:
+            raise ValueError(f"block table of sequence {s} points past the cache")
+
+
+def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 block_tables: torch.Tensor, seq_lens: torch.Tensor, scale: float, *,
+                 kv_dtype: Optional[int] = None, k_scale: float = 1.0, v_scale: float = 1.0,
+                 partition_size: int = 0, out: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None, validate: bool = True,
+                 stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """Decode attention through rllm_paged_attention_decode_ex."""
+    B, hq, d = q.shape
+    _check_common(q, k_cache, v_cache, block_tables, seq_lens, B)
+    nb, hkv, d2, bs = k_cache.shape
+    kv = _kv_code(k_cache, kv_dtype)
+    qd = _TORCH_16[q.dtype]
+    if kv in (DTYPE_F16, DTYPE_BF16) and kv != qd:
+        raise TypeError("a 16-bit cache must have the dtype of q")
+    if validate:
+        validate_tables(block_tables, seq_lens, nb, bs)
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous() or out.device != q.device:
+        raise ValueError("out must be a contiguous tensor like q")
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    call("rllm_paged_attention_decode_ex", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache),
+         _ptr(block_tables), _ptr(seq_lens), B, hq, hkv, d, bs, block_tables.shape[1], scale,
+         qd, kv, k_scale, v_scale, partition_size, _ptr(workspace), ws_bytes, _stream(stream))
+    return out
+
+
+def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  block_tables: torch.Tensor, seq_lens: torch.Tensor,
+                  query_start_loc: torch.Tensor, scale: float, *, kv_dtype: Optional[int] = None,
+                  k_scale: float = 1.0, v_scale: float = 1.0, out: Optional[torch.Tensor] = None,
+                  validate: bool = True,
+                  stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """Chunked-prefill attention through rllm_paged_attention_prefill_ex."""
+    T, hq, d = q.shape
+    B = seq_lens.shape[0]
+    _check_common(q, k_cache, v_cache, block_tables, seq_lens, B)
+    if query_start_loc.dtype != torch.int32 or query_start_loc.shape != (B + 1,) or \
+            query_start_loc.device != q.device:
+        raise ValueError("query_start_loc must be int32 [num_seqs + 1] on the device of q")
+    nb, hkv, d2, bs = k_cache.shape
+    kv = _kv_code(k_cache, kv_dtype)
+    qd = _TORCH_16[q.dtype]
+    if kv in (DTYPE_F16, DTYPE_BF16) and kv != qd:
+        raise TypeError("a 16-bit cache must have the dtype of q")
+    if validate:
+        validate_tables(block_tables, seq_lens, nb, bs)
+        qsl = query_start_loc.detach().cpu()
+        if int(qsl[0]) != 0 or int(qsl[-1]) != T or bool((qsl[1:] < qsl[:-1]).any()):
+            raise ValueError("query_start_loc must rise from 0 to num_tokens")
+    if out is None:
+        out = torch.empty_like(q)
+    call("rllm_paged_attention_prefill_ex", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache),
+         _ptr(block_tables), _ptr(seq_lens), _ptr(query_start_loc), B, T, hq, hkv, d, bs,
+         block_tables.shape[1], scale, qd, kv, k_scale, v_scale, _stream(stream))
+    return out
+
+
+def reshape_and_cache(new_key: torch.Tensor, new_value: torch.Tensor, k_cache: torch.Tensor,
+                      v_cache: torch.Tensor, slot_mapping: torch.Tensor, *,
+                      kv_dtype: Optional[int] = None, k_scale: float = 1.0, v_scale: float = 1.0,
+                      stream: Optional[torch.cuda.Stream] = None) -> None:
+    """Slot-mapped cache write through rllm_cache_write_{bf16,f16,fp8_scaled}."""
+    if new_key.shape != new_value.shape or new_key.dim() != 3:
+        raise ValueError("new_key/new_value must be [num_tokens, Hkv, D]")
+    n, hkv, d = new_key.shape
+    nb, hkv2, d2, bs = k_cache.shape
+    if (hkv, d) != (hkv2, d2) or k_cache.shape != v_cache.shape:
+        raise ValueError("token rows do not match the cache layout")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.shape != (n,):
+        raise ValueError("slot_mapping must be int64 [num_tokens]")
+    for t in (new_key, new_value, k_cache, v_cache, slot_mapping):
+        if not t.is_contiguous() or t.device != new_key.device:
+            raise ValueError("tensors must be contiguous and on one device")
+    kv = _kv_code(k_cache, kv_dtype)
+    ind = _TORCH_16.get(new_key.dtype)
+    if ind is None or new_value.dtype != new_key.dtype:
+        raise TypeError("new_key/new_value must be float16 or bfloat16")
+    st = _stream(stream)
+    if kv in (DTYPE_F16, DTYPE_BF16):
+        if kv != ind:
+            raise TypeError("16-bit cache dtype must equal the input dtype")
+        name = "rllm_cache_write_bf16" if kv == DTYPE_BF16 else "rllm_cache_write_f16"
+        call(name, _ptr(k_cache), _ptr(v_cache), _ptr(new_key), _ptr(new_value),
+             _ptr(slot_mapping), n, hkv, d, bs, nb, st)
+    else:
+        call("rllm_cache_write_fp8_scaled", _ptr(k_cache), _ptr(v_cache), _ptr(new_key),
+             _ptr(new_value), _ptr(slot_mapping), n, hkv, d, bs, nb, ind, k_scale, v_scale,
+             1 if kv == DTYPE_FP8_E5M2 else 0, st)

@@ -1,0 +1,112 @@
+"""Shared test helpers: an independent dense numpy formulation of paged
+attention (used to pin the C oracle), tolerance checks and small-case builders."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+
+# tolerances stated by the task: bf16 |a-b| <= 2e-2 + 1e-2|b|, FP8 KV 5e-2 + 5e-2|b|
+TOL_BF16 = (2e-2, 1e-2)
+TOL_FP8 = (5e-2, 5e-2)
+
+
+def gather_dense(cache_f: np.ndarray, bt_row: np.ndarray, ctx: int, h: int, bs: int):
+    """[n, D] rows of kv head h for logical tokens 0..ctx-1 (numpy fancy indexing),
+    skipping tokens whose block id is negative; also returns their positions."""
+    t = np.arange(ctx)
+    blk_ids = bt_row[t // bs]
+    keep = blk_ids >= 0
+    t = t[keep]
+    rows = cache_f[bt_row[t // bs], h, :, t % bs]  # [n, D]
+    return rows, t
+
+
+def dense_decode_f64(q_f, k_f, v_f, bt, seq_lens, scale):
+    """softmax(scale q.K^T) V per (seq, q head), float64, from decoded float arrays."""
+    B, hq, D = q_f.shape
+    nb, hkv, _, bs = k_f.shape
+    G = hq // hkv
+    out = np.zeros((B, hq, D), np.float64)
+    for s in range(B):
+        ctx = min(int(seq_lens[s]), bt.shape[1] * bs)
+        for h in range(hkv):
+            K, _ = gather_dense(k_f, bt[s], ctx, h, bs)
+            V, _ = gather_dense(v_f, bt[s], ctx, h, bs)
+            if K.shape[0] == 0:
+                continue
+            for g in range(G):
+                sc = (K.astype(np.float64) @ q_f[s, h * G + g].astype(np.float64)) * scale
+                p = np.exp(sc - sc.max())
+                out[s, h * G + g] = (p @ V.astype(np.float64)) / p.sum()
+    return out
+
+
+def dense_prefill_f64(q_f, k_f, v_f, bt, seq_lens, qsl, scale):
+    T, hq, D = q_f.shape
+    nb, hkv, _, bs = k_f.shape
+    G = hq // hkv
+    out = np.zeros((T, hq, D), np.float64)
+    for s in range(len(seq_lens)):
+        ctx = int(seq_lens[s])
+        n = int(qsl[s + 1] - qsl[s])
+        for h in range(hkv):
+            K, pos = gather_dense(k_f, bt[s], ctx, h, bs)
+            V, _ = gather_dense(v_f, bt[s], ctx, h, bs)
+            for i in range(n):
+                lim = ctx - n + i
+                m = pos <= lim
+                if not m.any():
+                    continue
+                for g in range(G):
+                    sc = (K[m].astype(np.float64) @ q_f[qsl[s] + i, h * G + g].astype(np.float64)) * scale
+                    p = np.exp(sc - sc.max())
+                    out[qsl[s] + i, h * G + g] = (p @ V[m].astype(np.float64)) / p.sum()
+    return out
+
+
+def assert_close(got, ref, tol, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    atol, rtol = tol
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = err > bound
+    rel_l2 = float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+    msg = (f"{what}: max_abs={err.max():.3e} max_rel={np.max(err / np.maximum(np.abs(ref), 1e-6)):.3e} "
+           f"rel_l2={rel_l2:.3e} violations={int(bad.sum())}/{bad.size}")
+    assert not bad.any() and np.isfinite(got).all(), msg
+    return rel_l2
+
+
+def random_case(rng, B, hq, hkv, D, ctx_range, bs=16, extra_blocks=3, neg_blocks=0,
+                max_blocks=None):
+    """Small random decode case with permuted tables (-1 padded)."""
+    lo, hi = ctx_range
+    sl = rng.integers(lo, hi, size=B, endpoint=True).astype(np.int32)
+    nblk = (sl + bs - 1) // bs
+    maxb = max_blocks or max(int(nblk.max()), 1)
+    pool = int(nblk.sum()) + extra_blocks
+    perm = rng.permutation(pool).astype(np.int32)
+    bt = np.full((B, maxb), -1, np.int32)
+    p = 0
+    for s in range(B):
+        n = min(int(nblk[s]), maxb)
+        bt[s, :n] = perm[p:p + n]
+        p += n
+    for _ in range(neg_blocks):
+        s = rng.integers(0, B)
+        if nblk[s] > 1:
+            bt[s, rng.integers(0, min(nblk[s], maxb))] = -1
+    q = (rng.standard_normal((B, hq, D))).astype(np.float32)
+    k = (rng.standard_normal((pool, hkv, D, bs))).astype(np.float32)
+    v = (rng.standard_normal((pool, hkv, D, bs))).astype(np.float32)
+    return q, k, v, bt, sl
+
+
+def to_bits(x, kind):
+    return O.encode(x, kind)
+
+
+def from_bits(b, kind):
+    return O.decode(b, kind)
