@@ -187,6 +187,14 @@ def paged_attention_decode_bf16(output, query, key_cache, value_cache, block_tab
          max_num_blocks_per_seq, scale, stream)
 
 
+def paged_attention_decode_bf16_sync(output, query, key_cache, value_cache, block_tables,
+                                     seq_lens, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                     block_size, max_num_blocks_per_seq, scale):
+    call("rllm_paged_attention_decode_bf16_sync", output, query, key_cache, value_cache,
+         block_tables, seq_lens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+         max_num_blocks_per_seq, scale)
+
+
 def paged_attention_decode_ex(output, query, key_cache, value_cache, block_tables, seq_lens,
                               num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
                               max_num_blocks_per_seq, scale, q_dtype, kv_dtype, k_scale=1.0,
@@ -230,6 +238,16 @@ def paged_attention_prefill_fp8(output, query, key_cache, value_cache, block_tab
          block_size, max_num_blocks_per_seq, scale, 1 if is_e5m2 else 0, stream)
 
 
+def paged_attention_prefill_fp8_sync(output, query, key_cache, value_cache, block_tables,
+                                     seq_lens, query_start_loc, num_seqs, num_tokens,
+                                     num_q_heads, num_kv_heads, head_dim, block_size,
+                                     max_num_blocks_per_seq, scale, is_e5m2):
+    call("rllm_paged_attention_prefill_fp8_sync", output, query, key_cache, value_cache,
+         block_tables, seq_lens, query_start_loc, num_seqs, num_tokens, num_q_heads,
+         num_kv_heads, head_dim, block_size, max_num_blocks_per_seq, scale,
+         1 if is_e5m2 else 0)
+
+
 def paged_attention_prefill_bf16(output, query, key_cache, value_cache, block_tables, seq_lens,
                                  query_start_loc, num_seqs, num_tokens, num_q_heads,
                                  num_kv_heads, head_dim, block_size, max_num_blocks_per_seq,
@@ -237,6 +255,15 @@ def paged_attention_prefill_bf16(output, query, key_cache, value_cache, block_ta
     call("rllm_paged_attention_prefill_bf16", output, query, key_cache, value_cache,
          block_tables, seq_lens, query_start_loc, num_seqs, num_tokens, num_q_heads,
          num_kv_heads, head_dim, block_size, max_num_blocks_per_seq, scale, stream)
+
+
+def paged_attention_prefill_bf16_sync(output, query, key_cache, value_cache, block_tables,
+                                      seq_lens, query_start_loc, num_seqs, num_tokens,
+                                      num_q_heads, num_kv_heads, head_dim, block_size,
+                                      max_num_blocks_per_seq, scale):
+    call("rllm_paged_attention_prefill_bf16_sync", output, query, key_cache, value_cache,
+         block_tables, seq_lens, query_start_loc, num_seqs, num_tokens, num_q_heads,
+         num_kv_heads, head_dim, block_size, max_num_blocks_per_seq, scale)
 
 
 def paged_attention_prefill_ex(output, query, key_cache, value_cache, block_tables, seq_lens,

@@ -99,9 +99,10 @@ def test_cache_write_fp8_reference_symbol_codec_table(dev):
         gk = torch.zeros((nb, 1, 1, bs), dtype=torch.uint8, device=dev)
         gv = torch.zeros_like(gk)
         src = t16(xb.reshape(n, 1, 1), torch.float16, dev)
+        gsl = ti(sl, torch.int64, dev)    # keep alive across the call
         log_case(f"rllm_cache_write_fp8_sync e5m2={is_e5m2}")
-        C.cache_write_fp8_sync(ptr(gk), ptr(gv), ptr(src), ptr(src), ptr(ti(sl, torch.int64, dev)),
-                               n, 1, 1, bs, nb, is_e5m2)
+        C.cache_write_fp8_sync(ptr(gk), ptr(gv), ptr(src), ptr(src), ptr(gsl), n, 1, 1, bs, nb,
+                               is_e5m2)
         got = gk.cpu().numpy().reshape(-1)[:n]
         assert np.array_equal(got, O.encode(O.decode(xb, O.F16), kind))
         exact = np.isfinite(x) & (O.decode(xb, O.F16) == x)   # inputs exactly representable in f16
