@@ -122,9 +122,11 @@ int32_t rllm_paged_attention_decode_bf16_sync(uint16_t *output, const uint16_t *
  *   kv_dtype  q_dtype, RLLM_DTYPE_FP8_E4M3 or RLLM_DTYPE_FP8_E5M2
  *   k_scale, v_scale  per-tensor dequantisation scales of an FP8 cache
  *             (cache value = byte value * scale); ignored for 16-bit caches
- *   partition_size  context tokens per split-K partition: 0 = automatic,
- *             < 0 = single pass (one workgroup per sequence and kv head),
- *             > 0 = that many tokens (a multiple of 128)
+ *   partition_size  0 = automatic (stream split: every resident wave takes an
+ *             equal share of all sequences' cache blocks; sequences cut between
+ *             waves are merged by a second kernel), < 0 = single pass (one wave
+ *             per sequence and kv head), > 0 = context tokens per split-K
+ *             partition (a multiple of 512)
  *   workspace, workspace_bytes  split-K scratch of at least
  *             rllm_paged_attention_decode_workspace_size(...) bytes; NULL =
  *             use a library-owned buffer cached per (device, stream). */
@@ -139,10 +141,11 @@ int32_t rllm_paged_attention_decode_ex(void *output, const void *query, const vo
                                        int64_t workspace_bytes, uintptr_t stream);
 
 /* New: bytes of split-K workspace rllm_paged_attention_decode_ex needs for
- * these shapes (0 when one partition covers max_num_blocks_per_seq blocks);
- * negative on invalid arguments. */
+ * these shapes on the current device (0 when nothing is split); negative on
+ * invalid arguments. */
 int64_t rllm_paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num_q_heads,
-                                                   int64_t head_dim, int64_t block_size,
+                                                   int64_t num_kv_heads, int64_t head_dim,
+                                                   int64_t block_size,
                                                    int64_t max_num_blocks_per_seq,
                                                    int64_t partition_size);
 

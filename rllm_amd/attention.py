@@ -206,10 +206,11 @@ def paged_attention_decode_ex(output, query, key_cache, value_cache, block_table
          workspace, workspace_bytes, stream)
 
 
-def decode_workspace_size(num_seqs, num_q_heads, head_dim, block_size, max_num_blocks_per_seq,
-                          partition_size=0) -> int:
+def decode_workspace_size(num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                          max_num_blocks_per_seq, partition_size=0) -> int:
     return int(lib().rllm_paged_attention_decode_workspace_size(
-        num_seqs, num_q_heads, head_dim, block_size, max_num_blocks_per_seq, partition_size))
+        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_num_blocks_per_seq,
+        partition_size))
 
 
 def paged_attention_prefill_f16(output, query, key_cache, value_cache, block_tables, seq_lens,

@@ -87,7 +87,7 @@ def test_decode_rejects_unsupported_shapes_without_launch():
     assert L.rllm_paged_attention_decode_ex(P, P, P, P, P, P, 4, 32, 8, 128, 16, 64, 0.1, 1, 1,
                                             1.0, 1.0, 100, None, 0, 0) == 1
     assert L.rllm_paged_attention_decode_ex(P, P, P, P, P, P, 4, 32, 8, 128, 16, 64, 0.1, 1, 1,
-                                            1.0, 1.0, 128, P, 16, 0) == 1
+                                            1.0, 1.0, 512, P, 16, 0) == 1
     assert L.rllm_paged_attention_decode_ex(P, P, P, P, P, P, 4, 32, 8, 128, 16, 64,
                                             float("nan"), 1, 1, 1.0, 1.0, 0, None, 0, 0) == 1
 
@@ -119,13 +119,14 @@ def test_prefill_and_cache_write_reject_invalid():
 def test_workspace_size_query():
     L = rllm_amd.lib()
     # one partition covers the table: no workspace
-    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 128, 16, 8, 0) == 0
-    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 128, 16, 256, -1) == 0
+    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 128, 16, 8, 512) == 0
+    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 128, 16, 256, -1) == 0
     # 256 blocks = 4096 tokens in 512-token partitions: 8 partitions
-    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 128, 16, 256, 512) == \
+    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 128, 16, 256, 512) == \
         64 * 32 * 8 * (128 + 2) * 4
-    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 96, 16, 256, 0) == -1
-    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 128, 16, 256, 100) == -1
+    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 96, 16, 256, 512) == -1
+    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 128, 16, 256, 100) == -1
+    assert L.rllm_paged_attention_decode_workspace_size(64, 30, 8, 128, 16, 256, 512) == -1
 
 
 def test_errors_surface_as_kernel_error():

@@ -53,7 +53,7 @@ def test_decode_golden_fixtures(dev):
         z = np.load(f)
         qk, kk = int(z["q_kind"]), int(z["kv_kind"])
         tol = TOL_FP8 if kk in (O.FP8_E4M3, O.FP8_E5M2) else TOL_BF16
-        for part in (0, -1, 128):
+        for part in (0, -1, 512):
             got = run_case(dev, z["q"], qk, z["k_cache"], z["v_cache"], kk, z["block_tables"],
                            z["seq_lens"], float(z["scale"]), float(z["k_scale"]),
                            float(z["v_scale"]), part, os.path.basename(f))
@@ -71,7 +71,7 @@ def test_decode_shapes_vs_oracle(dev, D, G, kind):
     qb, kb, vb = O.encode(q, kind), O.encode(k, kind), O.encode(v, kind)
     scale = 1 / np.sqrt(D)
     ref = oracle_ref(qb, kind, kb, vb, kind, bt, sl, scale)
-    for part in (0, -1, 256):
+    for part in (0, -1, 512):
         got = run_case(dev, qb, kind, kb, vb, kind, bt, sl, scale, partition_size=part)
         assert_close(got, ref, TOL_BF16, f"D={D} G={G} kind={kind} part={part}")
         assert np.all(got[0] == 0)  # empty context -> zeros
@@ -167,7 +167,7 @@ def test_decode_config2_full_and_split_equivalence(dev):
     ref = O.paged_attention_decode(qb, O.BF16, kb, vb, O.BF16, w.block_tables, w.seq_lens, w.scale,
                                    precision=0)
     outs = {}
-    for part in (0, -1, 128, 256, 1024):
+    for part in (0, -1, 512, 1024, 2048):
         outs[part] = run_case(dev, qb, O.BF16, kb, vb, O.BF16, w.block_tables, w.seq_lens, w.scale,
                               partition_size=part, label="config2")
         rl2 = assert_close(outs[part], ref, TOL_BF16, f"config 2 part={part}")
@@ -221,7 +221,7 @@ def test_decode_on_side_stream_with_caller_workspace(dev):
     q, k, v, bt, sl = random_case(rng, 5, 16, 4, 128, (300, 1200))
     qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
     ref = oracle_ref(qb, O.BF16, kb, vb, O.BF16, bt, sl, 0.09)
-    nbytes = A.decode_workspace_size(5, 16, 128, 16, bt.shape[1], 256)
+    nbytes = A.decode_workspace_size(5, 16, 4, 128, 16, bt.shape[1], 512)
     assert nbytes > 0
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     s = torch.cuda.Stream()
@@ -230,11 +230,11 @@ def test_decode_on_side_stream_with_caller_workspace(dev):
     torch.cuda.synchronize()
     with torch.cuda.stream(s):
         log_case("side stream + workspace")
-        out = ops.paged_decode(gq, gk, gv, gbt, gsl, 0.09, partition_size=256, workspace=ws)
+        out = ops.paged_decode(gq, gk, gv, gbt, gsl, 0.09, partition_size=512, workspace=ws)
     s.synchronize()
     assert_close(f32(out), ref, TOL_BF16, "side stream")
     with pytest.raises(rllm_amd.KernelError):
-        ops.paged_decode(gq, gk, gv, gbt, gsl, 0.09, partition_size=256, workspace=ws[:16])
+        ops.paged_decode(gq, gk, gv, gbt, gsl, 0.09, partition_size=512, workspace=ws[:16])
 
 
 def test_decode_invalid_arguments(dev):
@@ -252,8 +252,8 @@ def test_decode_invalid_arguments(dev):
     kc8 = torch.zeros((4, 2, 64, 8), dtype=torch.bfloat16, device=dev)
     with pytest.raises(rllm_amd.KernelError):             # block_size 8 unsupported
         ops.paged_decode(q, kc8, kc8, bt, sl, 0.1)
-    with pytest.raises(rllm_amd.KernelError):             # partition not a multiple of 128
-        ops.paged_decode(q, kc, kc, bt, sl, 0.1, partition_size=100)
+    with pytest.raises(rllm_amd.KernelError):             # partition not a multiple of 512
+        ops.paged_decode(q, kc, kc, bt, sl, 0.1, partition_size=640)
     with pytest.raises(rllm_amd.KernelError):             # null pointers
         A.paged_attention_decode_bf16(0, 0, 0, 0, 0, 0, 2, 8, 2, 64, 16, 2, 0.1)
     A.paged_attention_decode_bf16(0, 0, 0, 0, 0, 0, 0, 8, 2, 64, 16, 2, 0.1)  # empty: rc 0
