@@ -123,13 +123,18 @@ int32_t rllm_paged_attention_decode_bf16_sync(uint16_t *output, const uint16_t *
  *   k_scale, v_scale  per-tensor dequantisation scales of an FP8 cache
  *             (cache value = byte value * scale); ignored for 16-bit caches
  *   partition_size  0 = automatic (stream split: every resident wave takes an
- *             equal share of all sequences' cache blocks; sequences cut between
- *             waves are merged by a second kernel), < 0 = single pass (one wave
- *             per sequence and kv head), > 0 = context tokens per split-K
- *             partition (a multiple of 512)
+ *             equal share of all sequences' cache blocks; a sequence cut
+ *             between waves is merged by the last wave to finish a piece of
+ *             it, in the same kernel), < 0 = single pass (one wave per
+ *             sequence and kv head), > 0 = context tokens per split-K
+ *             partition (a multiple of 512; a second kernel merges)
  *   workspace, workspace_bytes  split-K scratch of at least
  *             rllm_paged_attention_decode_workspace_size(...) bytes; NULL =
- *             use a library-owned buffer cached per (device, stream). */
+ *             use a library-owned buffer cached per (device, stream, mode).
+ *             With partition_size 0 the buffer holds arrival counters: it must
+ *             be zero-filled before its first such call (and again after any
+ *             other use); each completed call leaves it ready for the next.
+ *             Calls that share a workspace must not overlap in time. */
 int32_t rllm_paged_attention_decode_ex(void *output, const void *query, const void *key_cache,
                                        const void *value_cache, const int32_t *block_tables,
                                        const int32_t *seq_lens, int64_t num_seqs,

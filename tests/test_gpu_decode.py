@@ -237,6 +237,50 @@ def test_decode_on_side_stream_with_caller_workspace(dev):
         ops.paged_decode(gq, gk, gv, gbt, gsl, 0.09, partition_size=512, workspace=ws[:16])
 
 
+def test_decode_stream_mode_caller_workspace_reused(dev):
+    """Stream mode merges rows cut between waves through per-row arrival
+    counters in the workspace; a zero-filled caller workspace must come back
+    ready for the next call, so consecutive calls of different shapes on one
+    buffer all match the oracle."""
+    rng = np.random.default_rng(23)
+    cases = [random_case(rng, 9, 32, 8, 128, (200, 3000)),
+             random_case(rng, 3, 16, 4, 64, (1, 900), neg_blocks=2),
+             random_case(rng, 9, 32, 8, 128, (200, 3000))]
+    nbytes = max(A.decode_workspace_size(c[0].shape[0], c[0].shape[1], c[1].shape[1], c[0].shape[2],
+                                         16, c[3].shape[1], 0) for c in cases)
+    assert nbytes > 0
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    for i, (q, k, v, bt, sl) in enumerate(cases * 2):
+        qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
+        scale = 1 / np.sqrt(q.shape[2])
+        ref = oracle_ref(qb, O.BF16, kb, vb, O.BF16, bt, sl, scale)
+        log_case(f"stream workspace call {i} B={q.shape[0]} D={q.shape[2]}")
+        out = ops.paged_decode(t16(qb, torch.bfloat16, dev), t16(kb, torch.bfloat16, dev),
+                               t16(vb, torch.bfloat16, dev), ti(bt, torch.int32, dev),
+                               ti(sl, torch.int32, dev), scale, partition_size=0, workspace=ws)
+        torch.cuda.synchronize()
+        assert_close(f32(out), ref, TOL_BF16, f"stream workspace call {i}")
+
+
+@pytest.mark.parametrize("kind", [O.BF16, O.FP8_E4M3])
+def test_decode_long_rows_split_over_many_waves(dev, kind):
+    """Two 40k-token sequences: every (sequence, kv head) row is cut into
+    dozens of wave pieces that one merge combines."""
+    rng = np.random.default_rng(29 + kind)
+    q, k, v, bt, sl = random_case(rng, 2, 8, 2, 128, (39000, 41000))
+    qb = O.encode(q, O.BF16)
+    if kind == O.BF16:
+        kb, vb, ks, vs = O.encode(k, kind), O.encode(v, kind), 1.0, 1.0
+    else:
+        ks, vs = float(np.abs(k).max() / 448.0), float(np.abs(v).max() / 448.0)
+        kb = O.encode((k / np.float32(ks)).astype(np.float32), kind)
+        vb = O.encode((v / np.float32(vs)).astype(np.float32), kind)
+    ref = O.paged_attention_decode(qb, O.BF16, kb, vb, kind, bt, sl, 1 / np.sqrt(128), ks, vs,
+                                   precision=1)
+    got = run_case(dev, qb, O.BF16, kb, vb, kind, bt, sl, 1 / np.sqrt(128), ks, vs, 0, "long rows")
+    assert_close(got, ref, TOL_BF16 if kind == O.BF16 else TOL_FP8, f"long rows kind={kind}")
+
+
 def test_decode_invalid_arguments(dev):
     q = torch.zeros((2, 8, 96), dtype=torch.bfloat16, device=dev)
     kc = torch.zeros((4, 2, 96, 16), dtype=torch.bfloat16, device=dev)
