@@ -115,6 +115,7 @@ constexpr int DPP_QUAD_XOR1 = 0xB1;
 constexpr int DPP_QUAD_XOR2 = 0x4E;
 constexpr int DPP_ROW_HALF_MIRROR = 0x141;
 constexpr int DPP_ROW_MIRROR = 0x140;
+constexpr int DPP_ROW_ROR8 = 0x128;   // rotate by 8 within 16 lanes: lane i gets lane i ^ 8
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
