@@ -10,9 +10,16 @@ finds the previous step's KV in L2 / MALL.
 
 value      = algorithmic bytes per call / wall-clock time per step (GB/s)
 roofline   = algorithmic bytes / average decode-call duration measured with HIP
-             events on the launch stream, against the 8 TB/s HBM3E peak
+             events on the launch stream (one kernel launch per call in the
+             default mode), against the 8 TB/s HBM3E peak; "traffic" is the
+             HBM bytes per launch measured with rocprofv3 FETCH_SIZE +
+             WRITE_SIZE, scaled by the same counters on a copy of known size,
+             read from the committed summary in profiles/ (null if absent)
 cpu_baseline = the CPU oracle's fp32 decode (C, std threads) on the same
              inputs, timed on this host's cores (oracle/, checker only)
+
+--calibrate-copy-mib N runs the library's block copy over N MiB three times
+after the timed region, so a counter run can scale FETCH_SIZE/WRITE_SIZE.
 """
 from __future__ import annotations
 
@@ -28,6 +35,22 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_stream_bf16_config2_traffic.md")
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per decode launch from the committed counter summary: the
+    line `traffic_bytes_per_launch: N (workload W)`; None when absent."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    parts = line.split()
+                    if f"{workload})" in line:
+                        return int(parts[1])
+    except OSError:
+        pass
+    return None
 
 
 def _cores() -> int:
@@ -70,6 +93,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 6])
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="after timing, run the library block copy over this many MiB (counter scaling)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -178,12 +203,22 @@ def main() -> int:
         "seqs_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(w.name),
                      "kernel_ms": round(kernel_ms, 5),
                      "kernel_ms_p10_p90": [round(float(np.percentile(call_ms, 10)), 5),
                                            round(float(np.percentile(call_ms, 90)), 5)],
                      "algorithmic_bytes": nbytes},
     }
+    if args.calibrate_copy_mib > 0:
+        from rllm_amd import cache_ops
+        n = args.calibrate_copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            cache_ops.cache_block_copy(src.data_ptr(), dst.data_ptr(), n, 1, sh)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, qb, kb, vb)
     print(json.dumps(res), flush=True)
