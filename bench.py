@@ -85,12 +85,82 @@ def cpu_baseline(w, qb, kb, vb, reps: int = 5):
                       f"{int(w.seq_lens.sum())}), fp32, median of {len(times)} runs after 1 warm-up"}
 
 
+def bench_prefill(args, w, lib, dev) -> int:
+    """Config 5: MFMA chunked prefill (8 seqs x 512 new tokens on 2048 cached),
+    FLOP/s against the dense bf16 MFMA peak."""
+    import numpy as np
+    import torch
+
+    import rllm_amd
+    qb, kb, vb = workloads_host(w)
+    t16 = lambda b: torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(dev)
+    q = t16(qb)
+    pools = [(t16(kb), t16(vb))]
+    pools.append((pools[0][0].clone(), pools[0][1].clone()))
+    bt = torch.from_numpy(w.block_tables).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    qsl = torch.from_numpy(w.query_start_loc()).to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+    sh = int(stream.cuda_stream)
+    fn = lib.rllm_paged_attention_prefill_ex
+    T = int(w.num_tokens)
+
+    def step(i):
+        kp, vp = pools[i & 1]
+        rc = fn(out.data_ptr(), q.data_ptr(), kp.data_ptr(), vp.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                qsl.data_ptr(), w.num_seqs, T, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size,
+                w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, rllm_amd.DTYPE_BF16, 1.0, 1.0, sh)
+        if rc:
+            raise rllm_amd.KernelError(rc, "rllm_paged_attention_prefill_ex")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    call_ms = [a.elapsed_time(b) for a, b in zip(starts, ends)]
+    flops = w.prefill_flops()
+    ms_per_step = wall * 1e3 / args.steps
+    kernel_ms = float(np.mean(call_ms))
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    res = {
+        "metric": "chunked-prefill paged attention TFLOP/s (MFMA) at 8B shape",
+        "value": round(flops / (ms_per_step * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1) (seeded), random permuted block tables",
+        "config": {"workload": w.name, "config_index": w.index, "num_seqs": w.num_seqs,
+                   "num_tokens": T, "num_q_heads": w.num_q_heads, "num_kv_heads": w.num_kv_heads,
+                   "head_dim": w.head_dim, "block_size": w.block_size,
+                   "context_per_seq": int(w.seq_lens.max()), "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel_ms": round(kernel_ms, 5), "algorithmic_flops": int(flops)},
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def workloads_host(w):
+    from rllm_amd import workloads
+    return workloads.host_tensors(w)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 6])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
+                    help="BASELINE config: 2 (default) is the headline decode line; 5 is chunked prefill")
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -111,6 +181,8 @@ def main() -> int:
     lib = rllm_amd.lib()
     dev = torch.device("cuda:0")
     w = workloads.config(args.config)
+    if args.config == 5:
+        return bench_prefill(args, w, lib, dev)
     fp8 = w.kv_dtype.startswith("fp8")
     qb, kb, vb = workloads.host_tensors(w)
 

@@ -214,6 +214,18 @@ struct Piece {
 // that every window issues the same loads whether or not it has blocks.
 __device__ __align__(16) uint8_t g_empty_tile[128 * BS * 2] = {};
 
+// v + the value of lane l ^ 8 / l ^ 16 / l ^ 32 (DPP rotate within 16 lanes;
+// v_permlane16_swap / v_permlane32_swap exchange rows of 16 / halves of 32)
+__device__ __forceinline__ float xor_sum8(float v) { return v + dpp<DPP_ROW_ROR8>(v); }
+__device__ __forceinline__ float xor_sum16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor_sum32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // 32-bit mask of the even bits of a 64-bit lane mask (lane 2j -> bit j)
 __device__ __forceinline__ uint32_t even_bits(uint64_t x) {
     x &= 0x5555555555555555ull;
@@ -424,13 +436,24 @@ struct Attn {
 #pragma unroll
         for (int i = PFK; i < PFV; ++i) issue_v(i, vr[i]);
         // sum the head_dim slices: lanes l ^ 2NB, l ^ 4NB, ... hold the other
-        // slices of the same (block, token half)
-#pragma unroll 1
-        for (int m = 2 << w.lnb; m < 64; m <<= 1) {
+        // slices of the same (block, token half); VALU lane swaps, no LDS
+        if (w.lnb <= 2) {
 #pragma unroll
             for (int g = 0; g < G; ++g)
 #pragma unroll
-                for (int t = 0; t < 8; ++t) acc[g][t] += __shfl_xor(acc[g][t], m);
+                for (int t = 0; t < 8; ++t) acc[g][t] = xor_sum8(acc[g][t]);
+        }
+        if (w.lnb <= 3) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[g][t] = xor_sum16(acc[g][t]);
+        }
+        if (w.lnb <= 4) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[g][t] = xor_sum32(acc[g][t]);
         }
 
         // ---------------- softmax over the window ----------------
