@@ -248,7 +248,9 @@ def main() -> int:
     wall = time.perf_counter() - t0
     call_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
-    nbytes = w.decode_bytes()
+    # config 4a aliases one prefix in every table: its roofline counts each
+    # physical block once (the logical figure is reported beside it)
+    nbytes = w.decode_bytes(distinct=(w.index == 4))
     ms_per_step = wall * 1e3 / args.steps
     kernel_ms = float(np.mean(call_ms))
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
@@ -282,6 +284,8 @@ def main() -> int:
                                            round(float(np.percentile(call_ms, 90)), 5)],
                      "algorithmic_bytes": nbytes},
     }
+    if w.index == 4:
+        res["roofline"]["logical_bytes"] = w.decode_bytes()
     if args.calibrate_copy_mib > 0:
         from rllm_amd import cache_ops
         n = args.calibrate_copy_mib << 20
