@@ -17,9 +17,10 @@
 //               ([t][d], so one ds_read_b128 is an MFMA operand row): a
 //               staging thread loads 8 rows x 8 tokens, transposes them with
 //               v_perm and writes 8 16-byte token rows.  V is staged as stored
-//               ([block][d][t]).  Tiles are double-buffered and the next
-//               tile's global loads are in flight while the current one is
-//               computed.
+//               ([block][d][t]) with each row's 4-token quads XOR-swizzled by
+//               (d >> 2) & 3 against LDS bank conflicts.  Tiles are
+//               double-buffered and the next tile's global loads are in
+//               flight while the current one is computed.
 //   per wave  = 32 query rows (two 16-row MFMA tiles):
 //     S^T = K Q^T   v_mfma_f32_16x16x32 (A = K rows from LDS, B = Q in VGPRs)
 //     softmax       fp32, exp2 domain; each lane owns one query row of each
@@ -207,11 +208,13 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     for (int off = 1; off < 64; off <<= 1) minp = min(minp, __shfl_xor(minp, off));
 
     // ---- staging: a K unit is 8 rows x 8 tokens of one block (transposed in
-    // registers, written as 8 token rows of 8 head_dim values); a V unit is
-    // 8 16-byte chunks of the tile's V, UNITS chunks apart (coalesced) ----
+    // registers, written as 8 token rows of 8 head_dim values; consecutive
+    // lanes take consecutive row groups so 8 lanes write one 128-byte run); a
+    // V unit is 8 16-byte chunks of the tile's V, UNITS chunks apart
+    // (coalesced) ----
     const bool k_stager = tid < UNITS;
     const bool v_stager = tid >= UNITS && tid < 2 * UNITS;
-    const int kb = tid / (D / 4), kdg = (tid % (D / 4)) >> 1, ktg = tid & 1;
+    const int kb = tid / (D / 4), kdg = tid % (D / 8), ktg = (tid / (D / 8)) & 1;
     const int vu = tid - UNITS;
     uint4 sreg[8];
     auto tile_block = [&](int tile, int b) -> int {   // physical block, -1 if none
@@ -219,8 +222,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         return blk * PF_BS < kv_end ? bt[blk] : -1;
     };
     auto fetch = [&](int tile) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) sreg[i] = make_uint4(0, 0, 0, 0);
         if (k_stager) {
             int pb = -1;
 #pragma unroll
@@ -231,6 +232,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
                                     static_cast<int64_t>(8 * kdg) * PF_BS + 8 * ktg;
 #pragma unroll
                 for (int r = 0; r < 8; ++r) sreg[r] = load8<QKIND, KVKIND>(a.k_cache, off + r * PF_BS);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 8; ++r) sreg[r] = make_uint4(0, 0, 0, 0);
             }
         } else if (v_stager) {
 #pragma unroll
@@ -242,6 +246,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
                 if (pb >= 0)
                     sreg[i] = load8<QKIND, KVKIND>(
                         a.v_cache, (static_cast<int64_t>(pb) * a.num_kv_heads + h) * head_elems + 8 * c);
+                else
+                    sreg[i] = make_uint4(0, 0, 0, 0);
             }
         }
     };
@@ -260,11 +266,25 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
                 *reinterpret_cast<uint4*>(&k_lds[buf][PF_BS * kb + 8 * ktg + t][8 * kdg]) = o;
             }
         } else if (v_stager) {
+            // chunk c = tokens 8hf..8hf+7 of row d of its block; the row's
+            // 4-token quads are stored XOR-swizzled by f = (d >> 2) & 3 (see
+            // v_quad), so the chunk lands in slot hf ^ (f >> 1), halves
+            // swapped when f is odd
             uint16_t* vb = &v_lds[buf][0][0][0];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(vb + 8 * (i * UNITS + vu)) = sreg[i];
+            for (int i = 0; i < 8; ++i) {
+                const int c = i * UNITS + vu;     // chunk of the tile: (block, d, hf)
+                const int row = c >> 1, hf = c & 1;
+                const int f = (row >> 2) & 3;
+                const uint4 x = sreg[i];
+                const uint4 y = (f & 1) ? make_uint4(x.z, x.w, x.x, x.y) : x;
+                *reinterpret_cast<uint4*>(vb + PF_BS * row + 8 * (hf ^ (f >> 1))) = y;
+            }
         }
     };
+    // element offset within a V row of the 4-token quad q (rows are XOR-swizzled
+    // so the 16 rows one PV operand load touches fall in distinct banks)
+    auto v_quad = [](int d, int q) { return 4 * (q ^ ((d >> 2) & 3)); };
 
     f32x4 o[2][NDT];
 #pragma unroll
@@ -363,8 +383,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
                                                              pk[mt][4 * kk + 2], pk[mt][4 * kk + 3]));
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
-                const uint2 v0 = *reinterpret_cast<const uint2*>(&v_lds[buf][2 * kk][16 * dt + lr][4 * lq]);
-                const uint2 v1 = *reinterpret_cast<const uint2*>(&v_lds[buf][2 * kk + 1][16 * dt + lr][4 * lq]);
+                const int d = 16 * dt + lr;
+                const uint2 v0 = *reinterpret_cast<const uint2*>(&v_lds[buf][2 * kk][d][v_quad(d, lq)]);
+                const uint2 v1 = *reinterpret_cast<const uint2*>(&v_lds[buf][2 * kk + 1][d][v_quad(d, lq)]);
                 const vec va = __builtin_bit_cast(vec, make_uint4(v0.x, v0.y, v1.x, v1.y));
                 o[0][dt] = M::mma(va, pb_[0], o[0][dt]);
                 o[1][dt] = M::mma(va, pb_[1], o[1][dt]);
