@@ -13,14 +13,15 @@
 //   workgroup = 4 waves = 128 query rows of one (sequence, kv head): the
 //               G = Hq/Hkv heads of the GQA group x 128/G query tokens, so
 //               every K/V tile staged in LDS serves the whole group.
-//   KV tile   = 64 tokens (four cache blocks).  K is transposed into LDS
-//               ([t][d], so one ds_read_b128 is an MFMA operand row): a
-//               staging thread loads 8 rows x 8 tokens, transposes them with
-//               v_perm and writes 8 16-byte token rows.  V is staged as stored
-//               ([block][d][t]) with each row's 4-token quads XOR-swizzled by
-//               (d >> 2) & 3 against LDS bank conflicts.  Tiles are
-//               double-buffered and the next tile's global loads are in
-//               flight while the current one is computed.
+//   KV tile   = 64 tokens (four cache blocks), double-buffered in LDS in
+//               the cache's own layout ([block][d][16 tokens]).  Wave w copies
+//               block w of the next tile global -> LDS directly
+//               (global_load_lds, no registers) while the current tile is
+//               computed; FP8 caches go through registers for the exact
+//               conversion.  V rows keep their 16-byte halves XOR-swizzled by
+//               (d >> 3) & 1 against LDS bank conflicts.  The QK operand (8
+//               consecutive d of one token) comes from two transposing reads
+//               (ds_read_b64_tr_b16) of that layout.
 //   per wave  = 32 query rows (two 16-row MFMA tiles):
 //     S^T = K Q^T   v_mfma_f32_16x16x32 (A = K rows from LDS, B = Q in VGPRs)
 //     softmax       fp32, exp2 domain; each lane owns one query row of each
@@ -126,14 +127,25 @@ __device__ __forceinline__ uint4 load8(const void* base, int64_t elem_off) {
     }
 }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// 16 bytes per lane from global memory straight into LDS: lane L of the wave
+// writes lds_seg + 16L.  (Non-template wrappers: the kernel templates must
+// not name these target builtins directly, or the host pass drops them.)
+__device__ __forceinline__ void lds_copy16(const uint16_t* src, uint16_t* lds_seg) {
+    __builtin_amdgcn_global_load_lds(src, lds_seg, 16, 0, 0);
+}
+// Transposing LDS read: in each group of 16 lanes, lane j addresses 4
+// consecutive 16-bit values M[j][0..3]; lane i receives M[4k + i/4][i%4]
+// for k = 0..3.
+__device__ __forceinline__ v4i16 lds_read_tr16(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
+}
+
 // Source of the staging loads of a missing cache block (id < 0 or past the
 // context): zeros, so every load is unconditional and a skipped block's V
 // contributes nothing.  Sized for the largest tile (head_dim 128 x 16 tokens).
 __device__ __align__(16) uint16_t g_pf_zero[128 * 16];
-
-__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
-    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
 
 // max over the lanes l, l^16, l^32, l^48 (VALU lane swaps, no LDS)
 __device__ __forceinline__ float xor_max_16_32(float v) {
@@ -150,12 +162,21 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     constexpr int QT = PF_ROWS / G;   // query tokens per workgroup
     constexpr int NKS = D / 32;       // MFMA k-steps over head_dim
     constexpr int NDT = D / 16;       // 16-wide head_dim tiles of the output
-    constexpr int KROW = D + 8;       // padded LDS row of transposed K (elements)
-    constexpr int UNITS = PF_NBT * D / 4;   // 8x8 K sub-blocks of a tile (= 8-chunk V units)
-    static_assert(2 * UNITS <= 256 && UNITS % 64 == 0, "staging roles must be whole waves");
+    constexpr bool FP8 = KVKIND == KIND_FP8_E4M3 || KVKIND == KIND_FP8_E5M2;
+    constexpr int SEGS = D / 32;      // 1 KiB (64 lanes x 16 B) segments of a block's 16-bit tile
+    static_assert(PF_NBT == 4, "one cache block of each tile per wave");
 
-    __shared__ __align__(16) uint16_t k_lds[2][PF_KT][KROW];
-    __shared__ __align__(16) uint16_t v_lds[2][PF_NBT][D][PF_BS];
+    // K and V tiles as stored in the cache ([block][d][16 tokens], 16-bit);
+    // V rows keep their two 16-byte halves XOR-swizzled by (d >> 3) & 1
+    // Two separate buffers (not one array indexed by the tile's parity): the
+    // tile loop is unrolled by two so every access names its buffer, and the
+    // compiler can see that the reads of one never wait for the asynchronous
+    // copies into the other.
+    using TileBuf = uint16_t[PF_NBT][D][PF_BS];
+    __shared__ __align__(16) TileBuf k_lds0, k_lds1, v_lds0, v_lds1;
+    // bc is a literal at every call site once the unrolled loop is inlined
+    auto kbuf = [&](int bc) -> TileBuf& { return bc == 0 ? k_lds0 : k_lds1; };
+    auto vbuf = [&](int bc) -> TileBuf& { return bc == 0 ? v_lds0 : v_lds1; };
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -214,81 +235,59 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) minp = min(minp, __shfl_xor(minp, off));
 
-    // ---- staging: a K unit is 8 rows x 8 tokens of one block (transposed in
-    // registers, written as 8 token rows of 8 head_dim values; consecutive
-    // lanes take consecutive row groups so 8 lanes write one 128-byte run); a
-    // V unit is 8 16-byte chunks of the tile's V, UNITS chunks apart
-    // (coalesced) ----
-    const bool k_stager = tid < UNITS;
-    const bool v_stager = tid >= UNITS && tid < 2 * UNITS;
-    const int kb = tid / (D / 4), kdg = tid % (D / 8), ktg = (tid / (D / 8)) & 1;
-    const int vu = tid - UNITS;
-    uint4 sreg[8];
+    // ---- staging: wave w copies block w of each tile (its K and V tiles).
+    // 16-bit caches go global -> LDS directly (global_load_lds, 16 bytes a
+    // lane, lane L of a segment writes bytes 16L..16L+15); V's swizzle is
+    // applied by choosing each lane's source half.  FP8 caches are loaded
+    // into registers, converted exactly and written to the same layout. ----
     auto tile_block = [&](int tile, int b) -> int {   // physical block, -1 if none
         const int blk = tile * PF_NBT + b;
         return blk * PF_BS < kv_end ? bt[blk] : -1;
     };
-    // Every load is unconditional: a missing block reads g_pf_zero.
-    auto fetch = [&](int tile) {
-        int pbt[PF_NBT];   // the tile's physical blocks (wave-uniform)
+    auto v_half = [](int d, int hf) { return hf ^ ((d >> 3) & 1); };   // stored slot of V half hf of row d
+    constexpr int FP8_LOADS = FP8 ? D / 32 : 1;     // 8-byte fp8 chunks per lane per tensor
+    uint4 kreg[FP8_LOADS], vreg[FP8_LOADS];
+    auto fetch = [&](int tile, int bc) -> void {   // every load is unconditional
+        const int pb = tile_block(tile, wave);
+        const int64_t tb = pb >= 0 ? (static_cast<int64_t>(pb) * a.num_kv_heads + h) * head_elems : 0;
+        if constexpr (!FP8) {
+            const uint16_t* kb = pb >= 0 ? static_cast<const uint16_t*>(a.k_cache) + tb : g_pf_zero;
+            const uint16_t* vb = pb >= 0 ? static_cast<const uint16_t*>(a.v_cache) + tb : g_pf_zero;
 #pragma unroll
-        for (int b = 0; b < PF_NBT; ++b) pbt[b] = tile_block(tile, b);
-        if (k_stager) {
-            int pb = pbt[0];
+            for (int i = 0; i < SEGS; ++i) {
+                const int d = 32 * i + (lane >> 1), hf = lane & 1;
+                lds_copy16(kb + (d * PF_BS + 8 * hf), &kbuf(bc)[wave][32 * i][0]);
+                lds_copy16(vb + (d * PF_BS + 8 * v_half(d, hf)), &vbuf(bc)[wave][32 * i][0]);
+            }
+        } else {
+            const void* kb = pb >= 0 ? a.k_cache : static_cast<const void*>(g_pf_zero);
+            const void* vb = pb >= 0 ? a.v_cache : static_cast<const void*>(g_pf_zero);
 #pragma unroll
-            for (int b = 1; b < PF_NBT; ++b) pb = kb == b ? pbt[b] : pb;
-            const int64_t in_tile = static_cast<int64_t>(8 * kdg) * PF_BS + 8 * ktg;
-            const void* base = pb >= 0 ? a.k_cache : static_cast<const void*>(g_pf_zero);
-            const int64_t off = (pb >= 0 ? (static_cast<int64_t>(pb) * a.num_kv_heads + h) * head_elems : 0) + in_tile;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) sreg[r] = load8<QKIND, KVKIND>(base, off + r * PF_BS);
-        } else if (v_stager) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                constexpr int CPB = 2 * D;                 // 16-byte chunks per block
-                const int b = (i * PF_NBT) / 8;            // block of chunk i (uniform)
-                const int c = i * UNITS + vu - b * CPB;    // chunk within the block
-                const int pb = pbt[b];
-                const void* base = pb >= 0 ? a.v_cache : static_cast<const void*>(g_pf_zero);
-                const int64_t off = (pb >= 0 ? (static_cast<int64_t>(pb) * a.num_kv_heads + h) * head_elems : 0) + 8 * c;
-                sreg[i] = load8<QKIND, KVKIND>(base, off);
+            for (int i = 0; i < FP8_LOADS; ++i) {
+                const int c = 64 * i + lane;        // 8-token chunk: row c >> 1, half c & 1
+                kreg[i] = load8<QKIND, KVKIND>(kb, tb + 8 * c);
+                vreg[i] = load8<QKIND, KVKIND>(vb, tb + 8 * c);
             }
         }
     };
-    auto stage = [&](int buf) {
-        if (k_stager) {
-            // token t of the unit gets rows 8kdg..8kdg+7 as 4 (row 2e, row 2e+1) words
+    auto stage = [&](int bc) -> void {             // FP8 only: registers -> LDS
+        if constexpr (FP8) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
-                const int w = t >> 1;
-                uint4 o;
-                o.x = __builtin_amdgcn_perm(word_of(sreg[1], w), word_of(sreg[0], w), sel);
-                o.y = __builtin_amdgcn_perm(word_of(sreg[3], w), word_of(sreg[2], w), sel);
-                o.z = __builtin_amdgcn_perm(word_of(sreg[5], w), word_of(sreg[4], w), sel);
-                o.w = __builtin_amdgcn_perm(word_of(sreg[7], w), word_of(sreg[6], w), sel);
-                *reinterpret_cast<uint4*>(&k_lds[buf][PF_BS * kb + 8 * ktg + t][8 * kdg]) = o;
-            }
-        } else if (v_stager) {
-            // chunk c = tokens 8hf..8hf+7 of row d of its block; the row's
-            // 4-token quads are stored XOR-swizzled by f = (d >> 2) & 3 (see
-            // v_quad), so the chunk lands in slot hf ^ (f >> 1), halves
-            // swapped when f is odd
-            uint16_t* vb = &v_lds[buf][0][0][0];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int c = i * UNITS + vu;     // chunk of the tile: (block, d, hf)
-                const int row = c >> 1, hf = c & 1;
-                const int f = (row >> 2) & 3;
-                const uint4 x = sreg[i];
-                const uint4 y = (f & 1) ? make_uint4(x.z, x.w, x.x, x.y) : x;
-                *reinterpret_cast<uint4*>(vb + PF_BS * row + 8 * (hf ^ (f >> 1))) = y;
+            for (int i = 0; i < FP8_LOADS; ++i) {
+                const int c = 64 * i + lane, d = c >> 1, hf = c & 1;
+                *reinterpret_cast<uint4*>(&kbuf(bc)[wave][d][8 * hf]) = kreg[i];
+                *reinterpret_cast<uint4*>(&vbuf(bc)[wave][d][8 * v_half(d, hf)]) = vreg[i];
             }
         }
     };
-    // element offset within a V row of the 4-token quad q (rows are XOR-swizzled
-    // so the 16 rows one PV operand load touches fall in distinct banks)
-    auto v_quad = [](int d, int q) { return 4 * (q ^ ((d >> 2) & 3)); };
+    // element offset within a V row of the 4-token quad q
+    auto v_quad = [&](int d, int q) { return 8 * v_half(d, q >> 1) + 4 * (q & 1); };
+    // QK operand: K[token lr][d0..d0+3] for the 16 lanes of a group, by a
+    // transposing read of rows d0..d0+3 (lane j of the group points at row
+    // d0 + j/4, tokens 4(j%4)..4(j%4)+3)
+    auto k_rows4 = [&](int bc, int tt, int d0) -> v4i16 {
+        return lds_read_tr16(&kbuf(bc)[tt][d0 + (lr >> 2)][4 * (lr & 3)]);
+    };
 
     f32x4 o[2][NDT];
 #pragma unroll
@@ -302,12 +301,17 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     // still counted as outstanding on loop entry and every iteration's first
     // MFMA would wait for all loads in flight, the next tile's included
     __builtin_amdgcn_s_waitcnt(0);
-    if (ntiles > 0) fetch(0);
-    for (int tile = 0; tile < ntiles; ++tile) {
-        const int buf = tile & 1;
-        stage(buf);
+    if (ntiles > 0) fetch(0, 0);
+    // one KV tile, computed from buffer bc while the next tile is copied into
+    // the other buffer
+    auto step = [&](int tile, int bc) -> void {
+        stage(bc);
+        // this wave's copies into bc are complete, then every wave's (and
+        // every wave is done reading the other buffer, which the next copies
+        // overwrite)
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tile + 1 < ntiles) fetch(tile + 1);
+        if (tile + 1 < ntiles) fetch(tile + 1, 1 - bc);
 
         const int t_base = tile * PF_KT;
         int pbv[PF_NBT];
@@ -327,7 +331,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
             st[tt][0] = st[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k < NKS; ++k) {
-                const vec ka = *reinterpret_cast<const vec*>(&k_lds[buf][16 * tt + lr][32 * k + 8 * lq]);
+                const v4i16 k0 = k_rows4(bc, tt, 32 * k + 8 * lq);
+                const v4i16 k1 = k_rows4(bc, tt, 32 * k + 8 * lq + 4);
+                const vec ka = __builtin_bit_cast(vec, __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7));
                 st[tt][0] = M::mma(ka, qreg[0][k], st[tt][0]);
                 st[tt][1] = M::mma(ka, qreg[1][k], st[tt][1]);
             }
@@ -392,13 +398,17 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
                 const int d = 16 * dt + lr;
-                const uint2 v0 = *reinterpret_cast<const uint2*>(&v_lds[buf][2 * kk][d][v_quad(d, lq)]);
-                const uint2 v1 = *reinterpret_cast<const uint2*>(&v_lds[buf][2 * kk + 1][d][v_quad(d, lq)]);
+                const uint2 v0 = *reinterpret_cast<const uint2*>(&vbuf(bc)[2 * kk][d][v_quad(d, lq)]);
+                const uint2 v1 = *reinterpret_cast<const uint2*>(&vbuf(bc)[2 * kk + 1][d][v_quad(d, lq)]);
                 const vec va = __builtin_bit_cast(vec, make_uint4(v0.x, v0.y, v1.x, v1.y));
                 o[0][dt] = M::mma(va, pb_[0], o[0][dt]);
                 o[1][dt] = M::mma(va, pb_[1], o[1][dt]);
             }
         }
+    };
+    for (int tile = 0; tile < ntiles; tile += 2) {
+        step(tile, 0);
+        if (tile + 1 < ntiles) step(tile + 1, 1);
     }
 
     // ---- normalise and store: lane holds out[row][16dt + 4lq + r] ----
