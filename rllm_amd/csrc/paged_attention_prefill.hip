@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     auto vbuf = [&](int bc) -> TileBuf& { return bc == 0 ? v_lds0 : v_lds1; };
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;   // wave is uniform
     const int lr = lane & 15, lq = lane >> 4;
 
     // ---- which (kv head, sequence, query tile) ----
