@@ -245,6 +245,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         return blk * PF_BS < kv_end ? bt[blk] : -1;
     };
     auto v_half = [](int d, int hf) { return hf ^ ((d >> 3) & 1); };   // stored slot of V half hf of row d
+    // K rows are permuted within each 16-row group (an involution): the two
+    // 16-lane groups of one transposing-read pass read rows 8 apart, which
+    // this puts 128 bytes apart, in different bank halves
+    auto k_slot = [](int d) { return d ^ (((d >> 3) & 1) << 2); };
     constexpr int FP8_LOADS = FP8 ? D / 32 : 1;     // 8-byte fp8 chunks per lane per tensor
     uint4 kreg[FP8_LOADS], vreg[FP8_LOADS];
     auto fetch = [&](int tile, int bc) -> void {   // every load is unconditional
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < SEGS; ++i) {
                 const int d = 32 * i + (lane >> 1), hf = lane & 1;
-                lds_copy16(kb + (d * PF_BS + 8 * hf), &kbuf(bc)[wave][32 * i][0]);
+                lds_copy16(kb + (k_slot(d) * PF_BS + 8 * hf), &kbuf(bc)[wave][32 * i][0]);
                 lds_copy16(vb + (d * PF_BS + 8 * v_half(d, hf)), &vbuf(bc)[wave][32 * i][0]);
             }
         } else {
@@ -275,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < FP8_LOADS; ++i) {
                 const int c = 64 * i + lane, d = c >> 1, hf = c & 1;
-                *reinterpret_cast<uint4*>(&kbuf(bc)[wave][d][8 * hf]) = kreg[i];
+                *reinterpret_cast<uint4*>(&kbuf(bc)[wave][k_slot(d)][8 * hf]) = kreg[i];
                 *reinterpret_cast<uint4*>(&vbuf(bc)[wave][d][8 * v_half(d, hf)]) = vreg[i];
             }
         }
@@ -286,7 +290,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     // transposing read of rows d0..d0+3 (lane j of the group points at row
     // d0 + j/4, tokens 4(j%4)..4(j%4)+3)
     auto k_rows4 = [&](int bc, int tt, int d0) -> v4i16 {
-        return lds_read_tr16(&kbuf(bc)[tt][d0 + (lr >> 2)][4 * (lr & 3)]);
+        return lds_read_tr16(&kbuf(bc)[tt][k_slot(d0 + (lr >> 2))][4 * (lr & 3)]);
     };
 
     f32x4 o[2][NDT];
@@ -339,52 +343,66 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
             }
         }
 
-        // ---- online softmax; lane owns query row lr of each m tile ----
-        uint32_t pk[2][2 * PF_NBT];
+        // ---- online softmax; lane owns query row lr of each m tile.  Both m
+        // tiles are handled in one branch so their dependency chains
+        // interleave ----
+        constexpr int NE = 4 * PF_NBT;
+        float p[2][NE], m_new[2];
+        if (full) {
+            // no mask; scale > 0, so the max of the raw scores gives the max
+            float mx[2];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            constexpr int NE = 4 * PF_NBT;
-            float p[NE];
-            float m_new;
-            if (full) {
-                // no mask; scale > 0, so the max of the raw scores gives the max
-                float mx = st[0][mt][0];
+            for (int mt = 0; mt < 2; ++mt) {
+                mx[mt] = st[0][mt][0];
 #pragma unroll
-                for (int e = 1; e < NE; ++e) mx = fmaxf(mx, st[e >> 2][mt][e & 3]);
-                mx = xor_max_16_32(mx);
-                m_new = fmaxf(m_run[mt], mx * c);
+                for (int e = 1; e < NE; ++e) mx[mt] = fmaxf(mx[mt], st[e >> 2][mt][e & 3]);
+            }
 #pragma unroll
-                for (int e = 0; e < NE; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(st[e >> 2][mt][e & 3], c, -m_new));
-            } else {
-                float sv[NE];
-                float mx = -INFINITY;
+            for (int mt = 0; mt < 2; ++mt) m_new[mt] = fmaxf(m_run[mt], xor_max_16_32(mx[mt]) * c);
+#pragma unroll
+            for (int e = 0; e < NE; ++e)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+                    p[mt][e] = __builtin_amdgcn_exp2f(fmaf(st[e >> 2][mt][e & 3], c, -m_new[mt]));
+        } else {
+            float sv[2][NE], mx[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int e = 0; e < NE; ++e) {
                     const int tt = e >> 2, r = e & 3;
                     const int t = t_base + 16 * tt + 4 * lq + r;
                     const bool ok = pbv[tt] >= 0 && t <= pos[mt] && t < kv_end;
-                    sv[e] = ok ? st[tt][mt][r] * c : -INFINITY;
-                    mx = fmaxf(mx, sv[e]);
+                    sv[mt][e] = ok ? st[tt][mt][r] * c : -INFINITY;
+                    mx[mt] = fmaxf(mx[mt], sv[mt][e]);
                 }
-                mx = xor_max_16_32(mx);
-                m_new = fmaxf(m_run[mt], mx);
-                const bool none = m_new == -INFINITY;
 #pragma unroll
-                for (int e = 0; e < NE; ++e) p[e] = none ? 0.f : __builtin_amdgcn_exp2f(sv[e] - m_new);
+            for (int mt = 0; mt < 2; ++mt) {
+                m_new[mt] = fmaxf(m_run[mt], xor_max_16_32(mx[mt]));
+                const bool none = m_new[mt] == -INFINITY;
+#pragma unroll
+                for (int e = 0; e < NE; ++e) p[mt][e] = none ? 0.f : __builtin_amdgcn_exp2f(sv[mt][e] - m_new[mt]);
             }
-            const float alpha = m_new == m_run[mt] ? 1.f : __builtin_amdgcn_exp2f(m_run[mt] - m_new);
+        }
+        float alpha[2];
+        uint32_t pk[2][2 * PF_NBT];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            alpha[mt] = m_new[mt] == m_run[mt] ? 1.f : __builtin_amdgcn_exp2f(m_run[mt] - m_new[mt]);
             float psum = 0.f;
 #pragma unroll
-            for (int e = 0; e < NE; ++e) psum += p[e];
-            l_run[mt] = l_run[mt] * alpha + psum;
-            m_run[mt] = m_new;
-            // the output accumulators change only when some row's max moved
-            if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+            for (int e = 0; e < NE; ++e) psum += p[mt][e];
+            l_run[mt] = l_run[mt] * alpha[mt] + psum;
+            m_run[mt] = m_new[mt];
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) o[mt][dt] *= alpha;
-            }
+            for (int e = 0; e < 2 * PF_NBT; ++e) pk[mt][e] = M::pack2(p[mt][2 * e], p[mt][2 * e + 1]);
+        }
+        // the output accumulators change only when some row's max moved
+        if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f)) {
 #pragma unroll
-            for (int e = 0; e < 2 * PF_NBT; ++e) pk[mt][e] = M::pack2(p[2 * e], p[2 * e + 1]);
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) o[mt][dt] *= alpha[mt];
         }
 
         // ---- O^T = V^T P^T: k-step kk covers t tiles 2kk and 2kk+1 ----
