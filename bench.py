@@ -165,6 +165,81 @@ def bench_prefill(args, w, lib, dev) -> int:
     return 0
 
 
+def bench_rope_cache(args, w, lib, dev) -> int:
+    """--op rope_cache: the fused RoPE + reshape_and_cache over the step's new
+    tokens of config w (decode configs: one token per sequence; config 5: the
+    4096-token prefill chunk), GB/s of algorithmic bytes against HBM peak.
+    Four input sets rotate so that no launch finds its inputs in the 256 MB
+    last-level cache."""
+    import numpy as np
+    import torch
+
+    import rllm_amd
+    from rllm_amd import ops
+    T, hq, hkv, D, bs = w.num_tokens, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
+    fp8 = w.kv_dtype.startswith("fp8")
+    kv = (rllm_amd.DTYPE_FP8_E4M3 if w.kv_dtype == "fp8_e4m3" else rllm_amd.DTYPE_FP8_E5M2) if fp8 \
+        else rllm_amd.DTYPE_BF16
+    g = torch.Generator(device="cpu").manual_seed(w.index)
+    sets = []
+    for _ in range(4):
+        mk = lambda *sh: torch.randn(*sh, generator=g).to(torch.bfloat16).to(dev)
+        sets.append((mk(T, hq, D), mk(T, hkv, D), mk(T, hkv, D), torch.empty(T, hq, D, dtype=torch.bfloat16,
+                                                                          device=dev)))
+    kc = torch.zeros((w.num_blocks, hkv, D, bs), dtype=torch.uint8 if fp8 else torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    slots = torch.from_numpy(w.new_token_slots()).to(dev)
+    pos = torch.from_numpy(w.new_token_positions()).to(dev)
+    max_pos = int(w.seq_lens.max())
+    cos, sin = ops.rope_cache_tables(max_pos, D, 500000.0, device=dev)
+    stream = torch.cuda.current_stream()
+    sh = int(stream.cuda_stream)
+    fn = lib.rllm_rope_cache_write
+
+    def step(i):
+        q, k, v, qo = sets[i & 3]
+        rc = fn(qo.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                slots.data_ptr(), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(), T, hq, hkv, D, bs,
+                w.num_blocks, max_pos, rllm_amd.DTYPE_BF16, kv, 1.0, 1.0, sh)
+        if rc:
+            raise rllm_amd.KernelError(rc, "rllm_rope_cache_write")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    region_ms = ev0.elapsed_time(ev1)
+    call_ms = per_launch_ms(step, args.steps, stream)
+    nbytes = w.rope_cache_bytes()
+    ms_per_step = wall * 1e3 / args.steps
+    kernel_ms = region_ms / args.steps
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    res = {
+        "metric": "fused RoPE + reshape_and_cache GB/s (algorithmic bytes)",
+        "value": round(nbytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1) (seeded), slots of the config's tables",
+        "config": {"workload": w.name, "config_index": w.index, "op": "rope_cache", "num_tokens": T,
+                   "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": D, "block_size": bs,
+                   "kv_dtype": w.kv_dtype, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_ms": round(kernel_ms, 5),
+                     "per_launch_ms_p10_p50_p90": [round(float(np.percentile(call_ms, q)), 5) for q in (10, 50, 90)],
+                     "algorithmic_bytes": nbytes},
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def workloads_host(w):
     from rllm_amd import workloads
     return workloads.host_tensors(w)
@@ -178,6 +253,9 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
                     help="BASELINE config: 2 (default) is the headline decode line; 5 is chunked prefill")
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
+    ap.add_argument("--op", default="attention", choices=["attention", "rope_cache"],
+                    help="attention (default): the config's decode or prefill line; rope_cache: the fused "
+                         "RoPE + cache write over the config's new tokens")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
@@ -197,6 +275,8 @@ def main() -> int:
     lib = rllm_amd.lib()
     dev = torch.device("cuda:0")
     w = workloads.config(args.config)
+    if args.op == "rope_cache":
+        return bench_rope_cache(args, w, lib, dev)
     if args.config == 5:
         return bench_prefill(args, w, lib, dev)
     fp8 = w.kv_dtype.startswith("fp8")

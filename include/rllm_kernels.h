@@ -282,6 +282,40 @@ int32_t rllm_cache_write_fp8_scaled(uint8_t *key_cache, uint8_t *value_cache,
                                     int64_t num_blocks, int32_t input_dtype, float k_scale,
                                     float v_scale, int32_t is_e5m2, uintptr_t stream);
 
+/* New (additive): rotary position embedding fused with the cache write.  It
+ * replaces the model-side sequence RotaryEmbedding::apply (rope.rs:34-43,
+ * 57-82: q and k rotated by halves, x*cos + rotate_half(x)*sin in the
+ * activation dtype) followed by rllm_cache_write_* (cache_ops.cu:161-200,
+ * 322-364) with one launch.  fused.cu:168-256 (rllm_fused_rope_f16, an
+ * interleaved-pair rotation no caller binds) is not what the model computes.
+ *   q, q_out    [num_tokens, num_q_heads, head_dim] of dtype; q_out == q is
+ *               allowed (in place); both may be NULL when num_q_heads == 0
+ *   k, v        [num_tokens, num_kv_heads, head_dim] of dtype; the rotated k
+ *               and v go to the caches, k and v are not modified
+ *   positions   int32 [num_tokens], clamped to [0, max_position)
+ *   cos_cache,  f32 [max_position, head_dim/2] as RotaryEmbedding::new builds
+ *   sin_cache   them (rope.rs:13-33); cast to dtype before use
+ *   dtype       RLLM_DTYPE_F16 | RLLM_DTYPE_BF16
+ *   kv_dtype    dtype, RLLM_DTYPE_FP8_E4M3 or RLLM_DTYPE_FP8_E5M2 (FP8 bytes =
+ *               encode(x / scale), as rllm_cache_write_fp8_scaled)
+ * slot_mapping < 0 (padding) or a block >= num_blocks skips the cache write of
+ * that token; q is still rotated.  head_dim must be a multiple of 16, and q,
+ * q_out, k, v, cos_cache and sin_cache 16-byte aligned. */
+int32_t rllm_rope_cache_write(void *q_out, const void *q, const void *k, const void *v,
+                              void *key_cache, void *value_cache, const int64_t *slot_mapping,
+                              const int32_t *positions, const float *cos_cache,
+                              const float *sin_cache, int64_t num_tokens, int64_t num_q_heads,
+                              int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                              int64_t num_blocks, int64_t max_position, int32_t dtype,
+                              int32_t kv_dtype, float k_scale, float v_scale, uintptr_t stream);
+
+/* New (additive), host only: fills the f32 cos / sin tables
+ * [max_position, head_dim/2] that rllm_rope_cache_write reads, as
+ * RotaryEmbedding::new computes them (rope.rs:13-33: f64 angles, f32 store).
+ * Both pointers are HOST memory; no GPU call is made. */
+int32_t rllm_rope_tables(float *cos_cache, float *sin_cache, int64_t max_position,
+                         int64_t head_dim, float theta);
+
 /* Replaces rllm_cache_block_copy(_sync), cache_ops.cu:264-292; bound at
  * cache_ops.rs:80-94. */
 int32_t rllm_cache_block_copy(const uint8_t *src, uint8_t *dst, int64_t block_nbytes,

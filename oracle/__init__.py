@@ -61,6 +61,9 @@ def lib() -> ctypes.CDLL:
     L.orc_slot_mapping.argtypes = [P, i64, P, i64, i64, P]
     L.orc_cache_write.argtypes = [P, P, P, P, P, i64, i64, i64, i64, i64, c.c_int, c.c_int,
                                   c.c_float, c.c_float]
+    L.orc_rope_cache_build.argtypes = [P, P, i64, i64, c.c_float]
+    L.orc_rope_cache_write.argtypes = [P, P, P, P, P, P, P, P, P, P, i64, i64, i64, i64, i64,
+                                       i64, i64, c.c_int, c.c_int, c.c_float, c.c_float]
     L.orc_paged_attention_decode.argtypes = [P, P, c.c_int, P, P, c.c_int, P, P, i64, i64, i64,
                                              i64, i64, i64, c.c_float, c.c_float, c.c_float,
                                              c.c_int, c.c_int]
@@ -125,6 +128,35 @@ def cache_write(key_cache, value_cache, new_key, new_value, slot_mapping, block_
     lib().orc_cache_write(_p(key_cache), _p(value_cache), _p(np.ascontiguousarray(new_key)),
                           _p(np.ascontiguousarray(new_value)), _p(sm), sm.size, hkv, d, bs, nb,
                           in_kind, cache_kind, k_scale, v_scale)
+
+
+def rope_cache_build(max_position: int, head_dim: int, theta: float = 10000.0):
+    """(cos, sin) float32 [max_position, head_dim // 2] as rope.rs:13-33 builds them."""
+    cos = np.empty((max_position, head_dim // 2), np.float32)
+    sin = np.empty_like(cos)
+    lib().orc_rope_cache_build(_p(cos), _p(sin), max_position, head_dim, theta)
+    return cos, sin
+
+
+def rope_cache_write(q, k, v, key_cache, value_cache, slot_mapping, positions, cos, sin,
+                     in_kind: int, cache_kind: int, k_scale: float = 1.0, v_scale: float = 1.0):
+    """Rotate q (returned) and k in the activation dtype, then write the rotated
+    key and v into the numpy caches [nb, Hkv, D, bs] in place."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    T, hq, d = q.shape
+    nb, hkv, d2, bs = key_cache.shape
+    assert d2 == d and k.shape == (T, hkv, d) and v.shape == k.shape
+    sm = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    cos = np.ascontiguousarray(cos, dtype=np.float32)
+    sin = np.ascontiguousarray(sin, dtype=np.float32)
+    q_out = np.empty_like(q)
+    lib().orc_rope_cache_write(_p(q_out), _p(q), _p(k), _p(v), _p(key_cache), _p(value_cache),
+                               _p(sm), _p(pos), _p(cos), _p(sin), T, hq, hkv, d, bs, nb,
+                               cos.shape[0], in_kind, cache_kind, k_scale, v_scale)
+    return q_out
 
 
 # ---- attention -----------------------------------------------------------

@@ -63,6 +63,9 @@ SIGNATURES = {
     "rllm_cache_write_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _U],
     "rllm_cache_write_fp8_sync": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32],
     "rllm_cache_write_fp8_scaled": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _F, _F, _I32, _U],
+    "rllm_rope_cache_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                              _I64, _I64, _I32, _I32, _F, _F, _U],
+    "rllm_rope_tables": [_P, _P, _I64, _I64, _F],
     "rllm_cache_block_copy": [_P, _P, _I64, _I64, _U],
     "rllm_cache_block_copy_sync": [_P, _P, _I64, _I64],
     "rllm_cache_zero": [_P, _I64, _U],

@@ -80,6 +80,33 @@ class Workload:
         return int(4 * self.head_dim * self.num_q_heads * total)
 
 
+    def new_token_positions(self) -> np.ndarray:
+        """int32 [num_tokens]: positions of the step's new tokens (decode: the
+        last position of each sequence; prefill: the chunk after the cache)."""
+        q = self.query_lens if self.query_lens is not None else np.ones(self.num_seqs, np.int32)
+        out = [np.arange(c - n, c) for c, n in zip(self.seq_lens.tolist(), q.tolist())]
+        return np.concatenate(out).astype(np.int32)
+
+    def new_token_slots(self) -> np.ndarray:
+        """int64 [num_tokens]: the cache slots of the new tokens
+        (block_table[pos // bs] * bs + pos % bs, model_runner.rs:806-826)."""
+        q = self.query_lens if self.query_lens is not None else np.ones(self.num_seqs, np.int32)
+        pos = self.new_token_positions().astype(np.int64)
+        seq = np.repeat(np.arange(self.num_seqs), q)
+        bs = self.block_size
+        return self.block_tables[seq, pos // bs].astype(np.int64) * bs + pos % bs
+
+    def rope_cache_bytes(self) -> int:
+        """Algorithmic HBM bytes of one fused RoPE + cache write over the new
+        tokens: read q, k, v (2 B each) and the token's cos / sin row slice
+        (2 * D/2 * 4 B), its slot (8 B) and position (4 B); write the rotated q
+        (2 B) and the key / value cache entries (e_kv B each)."""
+        T, hq, hkv, d = self.num_tokens, self.num_q_heads, self.num_kv_heads, self.head_dim
+        e = self.kv_elem_bytes()
+        per = hq * d * 2 * 2 + hkv * d * 2 * 2 + hkv * d * 2 * e + d * 4 + 12
+        return int(T * per)
+
+
 def _rng(index: int) -> np.random.Generator:
     return np.random.default_rng(SEED_BASE ^ index)
 
