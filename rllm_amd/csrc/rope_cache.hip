@@ -20,15 +20,17 @@
 // natively or through f32.  Contraction is off in the rotation: a rounding sits
 // between each product and the sum, and no FMA may skip it.
 //
-// Design: grid (token, item chunk); an item is either a rotation item — 8
-// consecutive elements of the first half of one q or k head and their 8
-// partners in the second half, read with two 16-byte loads, the cos / sin row
-// slice with four — or a value item of 8 elements.  Rotated q goes to q_out
-// (16-byte stores, in place allowed); the rotated key and the value go down one
-// stride-bs column of their [D][bs] cache tile, as in the plain cache write.
-// The whole step reads (Hq + 2 Hkv) * D * 2 bytes per token plus the cos/sin
-// row and writes the same amount: a few hundred KiB per decode step, latency
-// bound, so the point is one launch instead of rope(q), rope(k) and the write.
+// Design: tokens go in groups of 16.  Per group, one workgroup per kv head
+// rotates k and copies v into LDS ([token][D + 8] 16-bit rows), then writes the
+// cache: when the 16 tokens fill a 16-aligned run of one block (every prefill
+// chunk) each lane stores one [D][bs] row segment with 16-byte stores, else
+// one element per (token, row).  One workgroup per token rotates q into q_out
+// (16-byte loads and stores, in place allowed).  A rotation item is 8 elements
+// of the first half of a head and their 8 partners in the second half; bf16
+// rounding uses the packed hardware conversion (v_cvt_pk_bf16_f32, RNE).
+// The step reads (Hq + 2 Hkv) * D * 2 bytes per token plus its cos / sin row
+// and writes Hq * D * 2 + 2 * Hkv * D * e_kv: at a 4096-token prefill chunk an
+// HBM-bound stream, at decode (64 tokens, 1.6 MB) launch-latency bound.
 #include "common.h"
 #include "../../include/rllm_kernels.h"
 
@@ -78,45 +80,85 @@ __device__ __forceinline__ uint8_t enc8(uint16_t bits, float scale) {
     return CACHE_KIND == KIND_FP8_E4M3 ? fp8_e4m3_encode(x) : fp8_e5m2_encode(x);
 }
 
-// Rotates the 8 pairs (src[j0 + i], src[j0 + half + i]) with the cos / sin
-// row slices cp[0..7], sp[0..7]; returns the two 8-element halves packed.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two f32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32; NaN
+// is quieted as (bits >> 16) | 0x40, the software rule of f32_to_bf16_bits)
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+
+// Rotates the 8 pairs (x1[i], x2[i]) — elements j0+i and j0+half+i of a head —
+// with cos / sin row slices c4, s4: y1 = x1*c - x2*s, y2 = x2*c + x1*s, every
+// product and sum rounded to the activation dtype.
+template <int IN_KIND>
+__device__ __forceinline__ void rotate_regs(const uint4 w1, const uint4 w2, const float4 c0, const float4 c1,
+                                            const float4 s0, const float4 s1, uint4& o1, uint4& o2) {
+    const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const uint32_t a2[4] = {w1.x, w1.y, w1.z, w1.w};
+    const uint32_t b2[4] = {w2.x, w2.y, w2.z, w2.w};
+    uint32_t y1[4], y2[4];
+    if constexpr (IN_KIND == KIND_BF16) {
+        // element pairs (2i, 2i+1) share one packed conversion per rounding
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t cw = bf16_pair(cs[2 * i], cs[2 * i + 1]);
+            const uint32_t sw = bf16_pair(sn[2 * i], sn[2 * i + 1]);
+            const float cl = bf16_lo(cw), ch = bf16_hi(cw), sl = bf16_lo(sw), sh = bf16_hi(sw);
+            const float al = bf16_lo(a2[i]), ah = bf16_hi(a2[i]), bl = bf16_lo(b2[i]), bh = bf16_hi(b2[i]);
+            // the products of two bf16 values are exact in f32; each is rounded
+            const uint32_t ac = bf16_pair(al * cl, ah * ch), bs = bf16_pair(bl * sl, bh * sh);
+            const uint32_t bc = bf16_pair(bl * cl, bh * ch), as = bf16_pair(al * sl, ah * sh);
+            y1[i] = bf16_pair(bf16_lo(ac) - bf16_lo(bs), bf16_hi(ac) - bf16_hi(bs));
+            y2[i] = bf16_pair(bf16_lo(bc) + bf16_lo(as), bf16_hi(bc) + bf16_hi(as));
+        }
+    } else {
+        uint16_t x1[8], x2[8], z1[8], z2[8];
+        unpack8(w1, x1);
+        unpack8(w2, x2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            // The compiler rewrites these f32 ops on f16-exact values as half
+            // ops (exact rewrites), after which it would fuse a product into
+            // the sum as a v_fma_f16 and skip the product's rounding:
+            // contraction stays off.
+#pragma clang fp contract(off)
+            const float c = r16<IN_KIND>(cs[i]), s = r16<IN_KIND>(sn[i]);
+            const float a = dec16<IN_KIND>(x1[i]), b = dec16<IN_KIND>(x2[i]);
+            // r16(-b*s) = -r16(b*s): rounding is symmetric
+            z1[i] = enc16<IN_KIND>(r16<IN_KIND>(a * c) - r16<IN_KIND>(b * s));
+            z2[i] = enc16<IN_KIND>(r16<IN_KIND>(b * c) + r16<IN_KIND>(a * s));
+        }
+        const uint4 p1 = pack8(z1), p2 = pack8(z2);
+        y1[0] = p1.x; y1[1] = p1.y; y1[2] = p1.z; y1[3] = p1.w;
+        y2[0] = p2.x; y2[1] = p2.y; y2[2] = p2.z; y2[3] = p2.w;
+    }
+    o1 = make_uint4(y1[0], y1[1], y1[2], y1[3]);
+    o2 = make_uint4(y2[0], y2[1], y2[2], y2[3]);
+}
+
+// Rotates elements j0 .. j0+7 and j0+half .. j0+half+7 of the head at src.
 template <int IN_KIND>
 __device__ __forceinline__ void rotate8(const uint16_t* src, int32_t j0, int32_t half,
                                         const float* cp, const float* sp, uint4& o1, uint4& o2) {
-    const float4 c0 = *reinterpret_cast<const float4*>(cp);
-    const float4 c1 = *reinterpret_cast<const float4*>(cp + 4);
-    const float4 s0 = *reinterpret_cast<const float4*>(sp);
-    const float4 s1 = *reinterpret_cast<const float4*>(sp + 4);
-    const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-    const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    uint16_t x1[8], x2[8], y1[8], y2[8];
-    unpack8(*reinterpret_cast<const uint4*>(src + j0), x1);
-    unpack8(*reinterpret_cast<const uint4*>(src + j0 + half), x2);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        // For f16 the compiler rewrites the f32 ops on 16-bit-exact values as
-        // half ops (exact rewrites), after which it would fuse a product into
-        // the sum as a v_fma_f16 and skip the product's rounding: contraction
-        // stays off.
-#pragma clang fp contract(off)
-        const float c = r16<IN_KIND>(cs[i]), s = r16<IN_KIND>(sn[i]);
-        const float a = dec16<IN_KIND>(x1[i]), b = dec16<IN_KIND>(x2[i]);
-        // first half: a*c + (-b)*s, second half: b*c + a*s; rounding is
-        // symmetric, so r16(-b*s) = -r16(b*s) and the first is a difference
-        y1[i] = enc16<IN_KIND>(r16<IN_KIND>(a * c) - r16<IN_KIND>(b * s));
-        y2[i] = enc16<IN_KIND>(r16<IN_KIND>(b * c) + r16<IN_KIND>(a * s));
-    }
-    o1 = pack8(y1);
-    o2 = pack8(y2);
+    const uint4 w1 = *reinterpret_cast<const uint4*>(src + j0);
+    const uint4 w2 = *reinterpret_cast<const uint4*>(src + j0 + half);
+    rotate_regs<IN_KIND>(w1, w2, *reinterpret_cast<const float4*>(cp), *reinterpret_cast<const float4*>(cp + 4),
+                         *reinterpret_cast<const float4*>(sp), *reinterpret_cast<const float4*>(sp + 4), o1, o2);
 }
 
 __device__ __forceinline__ int32_t clamp_pos(int32_t p, int32_t max_position) {
     return p < 0 ? 0 : (p >= max_position ? max_position - 1 : p);
 }
 
-// Workgroup (g, y) covers tokens 16g .. 16g+15.  y < Hkv: kv head y of those
-// tokens — rotated k and v staged in LDS as [token][D + 8], then written as
-// cache rows; y >= Hkv: a 256-item slice of the tokens' q rotations.
+// Workgroup b covers tokens 16g .. 16g+15 of group g = b / roles in role
+// r = b % roles (roles = Hkv + 16, or Hkv without q), so a group's kv and q
+// workgroups are dispatched together.  r < Hkv: kv head r of those tokens —
+// rotated k and v staged in LDS as [token][D + 8], then written as cache rows;
+// r >= Hkv: the q rotations of token r - Hkv (uniform position and cos / sin
+// row; lanes beyond Hq * D / 16 items idle).
 template <int IN_KIND, int CACHE_KIND, bool DIV>
 __global__ __launch_bounds__(ROPE_THREADS) void rope_cache_kernel(
     uint16_t* q_out, const uint16_t* q, const uint16_t* __restrict__ k,
@@ -124,34 +166,41 @@ __global__ __launch_bounds__(ROPE_THREADS) void rope_cache_kernel(
     const int64_t* __restrict__ slot_mapping, const int32_t* __restrict__ positions,
     const float* __restrict__ cos_cache, const float* __restrict__ sin_cache, int64_t num_tokens,
     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int64_t block_size,
-    int64_t num_blocks, int32_t max_position, float k_scale, float v_scale) {
+    int64_t num_blocks, int32_t max_position, float k_scale, float v_scale, int32_t roles) {
     extern __shared__ __align__(16) uint16_t lds[];   // [2][ROPE_GROUP][head_dim + 8]
     __shared__ int64_t s_base[ROPE_GROUP];             // cache index of (token, head 0, d 0), or -1
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * ROPE_GROUP;
+    const int32_t role = static_cast<int32_t>(blockIdx.x % roles);
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x / roles) * ROPE_GROUP;
     const int32_t n_tok = static_cast<int32_t>(num_tokens - t0 < ROPE_GROUP ? num_tokens - t0 : ROPE_GROUP);
     const int32_t half = head_dim >> 1;
     const int32_t per_head = head_dim >> 4;   // rotation items per head
 
-    if (static_cast<int32_t>(blockIdx.y) >= num_kv_heads) {
-        const int32_t per_tok = num_q_heads * per_head;
-        const int32_t item = (static_cast<int32_t>(blockIdx.y) - num_kv_heads) * ROPE_THREADS + threadIdx.x;
-        const int32_t tok = item / per_tok;
+    if (role >= num_kv_heads) {
+        // one token per q workgroup: position and cos / sin row are uniform
+        const int32_t tok = role - num_kv_heads;
         if (tok >= n_tok) return;
-        const int32_t r = item - tok * per_tok;
-        const int32_t hq = r / per_head;
-        const int32_t j0 = (r - hq * per_head) * 8;
         const int64_t t = t0 + tok;
         const int64_t pos = clamp_pos(positions[t], max_position);
-        uint4 o1, o2;
-        rotate8<IN_KIND>(q + (t * num_q_heads + hq) * head_dim, j0, half, cos_cache + pos * half + j0,
-                         sin_cache + pos * half + j0, o1, o2);
-        uint16_t* dst = q_out + (t * num_q_heads + hq) * head_dim;
-        *reinterpret_cast<uint4*>(dst + j0) = o1;
-        *reinterpret_cast<uint4*>(dst + j0 + half) = o2;
+        const float* crow = cos_cache + pos * half;
+        const float* srow = sin_cache + pos * half;
+        const uint16_t* qrow = q + t * num_q_heads * head_dim;
+        uint16_t* orow = q_out + t * num_q_heads * head_dim;
+        const int32_t per_tok = num_q_heads * per_head;
+        const int32_t sh = __builtin_ctz(static_cast<uint32_t>(per_head));
+        const bool pow2_ph = (per_head & (per_head - 1)) == 0;
+        for (int32_t r = threadIdx.x; r < per_tok; r += ROPE_THREADS) {
+            const int32_t hq = pow2_ph ? (r >> sh) : r / per_head;
+            const int32_t j0 = (r - hq * per_head) * 8;
+            uint4 o1, o2;
+            rotate8<IN_KIND>(qrow + static_cast<int64_t>(hq) * head_dim, j0, half, crow + j0, srow + j0, o1, o2);
+            uint16_t* dst = orow + static_cast<int64_t>(hq) * head_dim;
+            *reinterpret_cast<uint4*>(dst + j0) = o1;
+            *reinterpret_cast<uint4*>(dst + j0 + half) = o2;
+        }
         return;
     }
 
-    const int32_t h = blockIdx.y;
+    const int32_t h = role;
     const int32_t stride = head_dim + 8;   // LDS row in elements (16-byte pad)
     uint16_t* kl = lds;
     uint16_t* vl = lds + ROPE_GROUP * stride;
@@ -264,6 +313,7 @@ struct RopeArgs {
     int64_t bs, nb;
     int32_t maxp;
     float ks, vs;
+    int32_t roles;
 };
 
 template <int IN_KIND, int CACHE_KIND>
@@ -273,11 +323,11 @@ int32_t launch_rope(dim3 grid, hipStream_t st, const RopeArgs& a) {
     if (fp8 && !(pow2(a.ks) && pow2(a.vs)))
         hipLaunchKernelGGL((rope_cache_kernel<IN_KIND, CACHE_KIND, true>), grid, dim3(ROPE_THREADS), lds, st,
                            a.q_out, a.q, a.k, a.v, a.kc, a.vc, a.sm, a.pos, a.cs, a.sn, a.n, a.hq, a.hkv, a.d,
-                           a.bs, a.nb, a.maxp, a.ks, a.vs);
+                           a.bs, a.nb, a.maxp, a.ks, a.vs, a.roles);
     else
         hipLaunchKernelGGL((rope_cache_kernel<IN_KIND, CACHE_KIND, false>), grid, dim3(ROPE_THREADS), lds, st,
                            a.q_out, a.q, a.k, a.v, a.kc, a.vc, a.sm, a.pos, a.cs, a.sn, a.n, a.hq, a.hkv, a.d,
-                           a.bs, a.nb, a.maxp, fp8 ? 1.0f / a.ks : 1.0f, fp8 ? 1.0f / a.vs : 1.0f);
+                           a.bs, a.nb, a.maxp, fp8 ? 1.0f / a.ks : 1.0f, fp8 ? 1.0f / a.vs : 1.0f, a.roles);
     return launch_status();
 }
 
@@ -318,16 +368,17 @@ extern "C" int32_t rllm_rope_cache_write(void* q_out, const void* q, const void*
     if (kv_dtype == RLLM_DTYPE_FP8_E4M3 || kv_dtype == RLLM_DTYPE_FP8_E5M2)
         RLLM_CHECK_ARG(k_scale > 0.f && v_scale > 0.f && std::isfinite(k_scale) &&
                        std::isfinite(v_scale));
-    // grid: 16-token groups x (one workgroup per kv head + the q rotation slices)
+    // grid: 16-token groups x (one workgroup per kv head + one per token for q)
     const int64_t groups = (num_tokens + ROPE_GROUP - 1) / ROPE_GROUP;
-    const int64_t q_slices = (ROPE_GROUP * num_q_heads * (head_dim / 16) + ROPE_THREADS - 1) / ROPE_THREADS;
+    const int64_t q_slices = num_q_heads > 0 ? ROPE_GROUP : 0;
     RLLM_CHECK_ARG(num_kv_heads + q_slices <= 65535);
-    const dim3 grid(static_cast<unsigned>(groups), static_cast<unsigned>(num_kv_heads + q_slices));
+    RLLM_CHECK_ARG(groups * (num_kv_heads + q_slices) <= (int64_t(1) << 31) - 1);
+    const dim3 grid(static_cast<unsigned>(groups * (num_kv_heads + q_slices)));
     const RopeArgs a{static_cast<uint16_t*>(q_out), static_cast<const uint16_t*>(q),
                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), key_cache, value_cache,
                      slot_mapping, positions, cos_cache, sin_cache, num_tokens, (int32_t)num_q_heads,
                      (int32_t)num_kv_heads, (int32_t)head_dim, block_size, num_blocks, (int32_t)max_position,
-                     k_scale, v_scale};
+                     k_scale, v_scale, (int32_t)(num_kv_heads + q_slices)};
     hipStream_t st = as_stream(stream);
     if (dtype == RLLM_DTYPE_BF16) return dispatch_cache<KIND_BF16>(kv_dtype, grid, st, a);
     return dispatch_cache<KIND_F16>(kv_dtype, grid, st, a);
