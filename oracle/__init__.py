@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
     L.orc_slot_mapping.argtypes = [P, i64, P, i64, i64, P]
     L.orc_cache_write.argtypes = [P, P, P, P, P, i64, i64, i64, i64, i64, c.c_int, c.c_int,
                                   c.c_float, c.c_float]
+    L.orc_copy_blocks.argtypes = [P, P, i64, P, i64, i64, i64]
+    L.orc_swap_blocks.argtypes = [P, P, i64, P, i64, P, i64, i64, i64, P, c.c_int]
     L.orc_rope_cache_build.argtypes = [P, P, i64, i64, c.c_float]
     L.orc_rope_cache_write.argtypes = [P, P, P, P, P, P, P, P, P, P, i64, i64, i64, i64, i64,
                                        i64, i64, c.c_int, c.c_int, c.c_float, c.c_float]
@@ -128,6 +130,29 @@ def cache_write(key_cache, value_cache, new_key, new_value, slot_mapping, block_
     lib().orc_cache_write(_p(key_cache), _p(value_cache), _p(np.ascontiguousarray(new_key)),
                           _p(np.ascontiguousarray(new_value)), _p(sm), sm.size, hkv, d, bs, nb,
                           in_kind, cache_kind, k_scale, v_scale)
+
+
+def _ptr_array(arrays):
+    for a in arrays:
+        assert a.flags["C_CONTIGUOUS"]
+    return (ctypes.c_void_p * len(arrays))(*[a.ctypes.data for a in arrays])
+
+
+def copy_blocks(key_caches, value_caches, pairs, num_blocks: int, block_nbytes: int):
+    """In place on lists of per-layer numpy caches (any dtype, C-contiguous)."""
+    pr = np.ascontiguousarray(pairs, dtype=np.int64).reshape(-1, 2)
+    lib().orc_copy_blocks(_ptr_array(key_caches), _ptr_array(value_caches), len(key_caches),
+                          _p(pr), pr.shape[0], num_blocks, block_nbytes)
+
+
+def swap_blocks(key_caches, value_caches, ids, records, num_blocks: int, block_nbytes: int,
+                out: bool, slots=None):
+    """records: uint8 [num_records, layers, 2, block_nbytes] (modified when out)."""
+    ids = np.ascontiguousarray(ids, dtype=np.int64)
+    sl = None if slots is None else np.ascontiguousarray(slots, dtype=np.int64)
+    lib().orc_swap_blocks(_ptr_array(key_caches), _ptr_array(value_caches), len(key_caches),
+                          _p(ids), ids.size, None if sl is None else _p(sl), records.shape[0],
+                          num_blocks, block_nbytes, _p(records), 1 if out else 0)
 
 
 def rope_cache_build(max_position: int, head_dim: int, theta: float = 10000.0):

@@ -296,6 +296,50 @@ void orc_cache_write(void *key_cache, void *value_cache, const void *new_key,
 }
 
 /* ------------------------------------------------------------------ */
+/* block copy (copy-on-write) and swap records                          */
+/* ------------------------------------------------------------------ */
+
+/* cache_block_copy (cache_ops.cu:252-262) of one block per layer and K/V for
+ * each (src, dst) pair, in list order, as the caller of
+ * BlockPool::copy_on_write (block_pool.rs:286-302) would issue them. */
+void orc_copy_blocks(uint8_t *const *key_caches, uint8_t *const *value_caches, int64_t num_layers,
+                     const int64_t *pairs, int64_t num_pairs, int64_t num_blocks,
+                     int64_t block_nbytes) {
+    for (int64_t p = 0; p < num_pairs; p++) {
+        int64_t src = pairs[2 * p], dst = pairs[2 * p + 1];
+        if (src < 0 || dst < 0 || src >= num_blocks || dst >= num_blocks || src == dst) continue;
+        for (int64_t l = 0; l < num_layers; l++) {
+            memcpy(key_caches[l] + dst * block_nbytes, key_caches[l] + src * block_nbytes,
+                   (size_t)block_nbytes);
+            memcpy(value_caches[l] + dst * block_nbytes, value_caches[l] + src * block_nbytes,
+                   (size_t)block_nbytes);
+        }
+    }
+}
+
+/* One CpuKvOffloadStore record (offload.rs:28-74) per block: [layer][K, V]
+ * [block_nbytes]; id i uses record slots[i] (i when slots is NULL).  out != 0
+ * copies caches -> records, else records -> caches. */
+void orc_swap_blocks(uint8_t *const *key_caches, uint8_t *const *value_caches, int64_t num_layers,
+                     const int64_t *ids, int64_t num_ids, const int64_t *slots, int64_t num_records,
+                     int64_t num_blocks, int64_t block_nbytes, uint8_t *records, int out) {
+    for (int64_t i = 0; i < num_ids; i++) {
+        int64_t b = ids[i], r = slots ? slots[i] : i;
+        if (b < 0 || b >= num_blocks || r < 0 || r >= num_records) continue;
+        for (int64_t l = 0; l < num_layers; l++) {
+            for (int kv = 0; kv < 2; kv++) {
+                uint8_t *cache = (kv ? value_caches[l] : key_caches[l]) + b * block_nbytes;
+                uint8_t *rec = records + ((r * num_layers + l) * 2 + kv) * block_nbytes;
+                if (out)
+                    memcpy(rec, cache, (size_t)block_nbytes);
+                else
+                    memcpy(cache, rec, (size_t)block_nbytes);
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
 /* rotary embedding fused with the cache write                          */
 /* ------------------------------------------------------------------ */
 

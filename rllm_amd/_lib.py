@@ -66,6 +66,9 @@ SIGNATURES = {
     "rllm_rope_cache_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                               _I64, _I64, _I32, _I32, _F, _F, _U],
     "rllm_rope_tables": [_P, _P, _I64, _I64, _F],
+    "rllm_cache_copy_blocks": [_P, _P, _I64, _P, _I64, _I64, _I64, _U],
+    "rllm_cache_swap_out": [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _U],
+    "rllm_cache_swap_in": [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _U],
     "rllm_cache_block_copy": [_P, _P, _I64, _I64, _U],
     "rllm_cache_block_copy_sync": [_P, _P, _I64, _I64],
     "rllm_cache_zero": [_P, _I64, _U],

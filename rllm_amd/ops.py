@@ -229,3 +229,68 @@ def rope_and_cache(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor,
          _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), _ptr(positions), _ptr(cos), _ptr(sin),
          n, hq, hkv, d, bs, nb, cos.shape[0], dt, kv, k_scale, v_scale, _stream(stream))
     return q_out if q is not None else None
+
+
+def layer_table(caches, device) -> torch.Tensor:
+    """DEVICE uint64 array of the per-layer cache base addresses, the form
+    rllm_cache_copy_blocks / rllm_cache_swap_{out,in} take.  Build it once per
+    cache allocation and keep it alive while calls use it."""
+    return torch.tensor([int(c.data_ptr()) for c in caches], dtype=torch.int64).to(device)
+
+
+def _block_geometry(key_caches, value_caches):
+    if not key_caches or len(key_caches) != len(value_caches):
+        raise ValueError("need one key and one value cache per layer")
+    c0 = key_caches[0]
+    for c in list(key_caches) + list(value_caches):
+        if c.shape != c0.shape or c.dtype != c0.dtype or c.device != c0.device or not c.is_contiguous():
+            raise ValueError("all layer caches must share shape, dtype and device, contiguous")
+    nb = c0.shape[0]
+    return nb, c0[0].numel() * c0.element_size()
+
+
+def copy_blocks(key_caches, value_caches, block_pairs: torch.Tensor, *, tables=None,
+                stream: Optional[torch.cuda.Stream] = None) -> None:
+    """Copy-on-write data movement: block src -> dst of every (src, dst) row of
+    the int64 [n, 2] device tensor, in every layer's key and value cache
+    (rllm_cache_copy_blocks).  ``tables`` = (key, value) from layer_table()."""
+    nb, nbytes = _block_geometry(key_caches, value_caches)
+    if block_pairs.dtype != torch.int64 or block_pairs.dim() != 2 or block_pairs.shape[1] != 2 \
+            or not block_pairs.is_contiguous():
+        raise ValueError("block_pairs must be contiguous int64 [n, 2]")
+    dev = key_caches[0].device
+    kt, vt = tables if tables is not None else (layer_table(key_caches, dev), layer_table(value_caches, dev))
+    call("rllm_cache_copy_blocks", _ptr(kt), _ptr(vt), len(key_caches), _ptr(block_pairs),
+         block_pairs.shape[0], nb, nbytes, _stream(stream))
+
+
+def _swap(name, key_caches, value_caches, block_ids, records, slots, tables, stream):
+    nb, nbytes = _block_geometry(key_caches, value_caches)
+    L = len(key_caches)
+    if block_ids.dtype != torch.int64 or block_ids.dim() != 1 or not block_ids.is_contiguous():
+        raise ValueError("block_ids must be contiguous int64 [n]")
+    if records.dtype != torch.uint8 or records.device.type != "cpu" or not records.is_pinned() \
+            or not records.is_contiguous() or records.dim() != 4 \
+            or tuple(records.shape[1:]) != (L, 2, nbytes):
+        raise ValueError(f"records must be pinned contiguous uint8 [R, {L}, 2, {nbytes}]")
+    if slots is not None and (slots.dtype != torch.int64 or slots.shape != block_ids.shape):
+        raise ValueError("slots must be int64 like block_ids")
+    dev = key_caches[0].device
+    kt, vt = tables if tables is not None else (layer_table(key_caches, dev), layer_table(value_caches, dev))
+    call(name, _ptr(kt), _ptr(vt), L, _ptr(block_ids), block_ids.shape[0], nb, nbytes, _ptr(slots),
+         records.shape[0], _ptr(records), _stream(stream))
+
+
+def swap_out(key_caches, value_caches, block_ids: torch.Tensor, records: torch.Tensor, *,
+             slots: Optional[torch.Tensor] = None, tables=None,
+             stream: Optional[torch.cuda.Stream] = None) -> None:
+    """Blocks -> pinned host records [R, layers, 2, block_nbytes]
+    (rllm_cache_swap_out); synchronise before reading ``records``."""
+    _swap("rllm_cache_swap_out", key_caches, value_caches, block_ids, records, slots, tables, stream)
+
+
+def swap_in(key_caches, value_caches, block_ids: torch.Tensor, records: torch.Tensor, *,
+            slots: Optional[torch.Tensor] = None, tables=None,
+            stream: Optional[torch.cuda.Stream] = None) -> None:
+    """Pinned host records -> blocks (rllm_cache_swap_in)."""
+    _swap("rllm_cache_swap_in", key_caches, value_caches, block_ids, records, slots, tables, stream)
