@@ -240,6 +240,79 @@ def bench_rope_cache(args, w, lib, dev) -> int:
     return 0
 
 
+def bench_block_moves(args, w, lib, dev) -> int:
+    """--op copy_blocks / swap_out / swap_in: block-list data movement over a
+    32-layer cache with config w's block geometry (Llama-3-8B: 8 kv heads x
+    128 x 16 tokens, 32 KiB per block per K / V).  One step moves one tail
+    block per sequence of the config in every layer and K / V (copy_blocks:
+    copy-on-write forks; swap: to / from pinned offload records).  Bytes are
+    read + written bytes; copy_blocks is HBM-bound, the swaps are bound by the
+    host link."""
+    import numpy as np
+    import torch
+
+    import rllm_amd
+    from rllm_amd import ops
+    L, nb = 32, 1024
+    shape = (nb, w.num_kv_heads, w.head_dim, w.block_size)
+    kc = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    vc = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    nbytes = kc[0][0].numel() * 2
+    kt, vt = ops.layer_table(kc, dev), ops.layer_table(vc, dev)
+    n = w.num_seqs
+    rng = np.random.default_rng(w.index)
+    perm = rng.permutation(nb)
+    # two disjoint pair lists so consecutive steps touch different blocks
+    pair_sets = [torch.from_numpy(np.stack([perm[i * 2 * n:i * 2 * n + n], perm[i * 2 * n + n:(i + 1) * 2 * n]],
+                                           axis=1).astype(np.int64)).to(dev) for i in range(2)]
+    id_sets = [p[:, 0].contiguous() for p in pair_sets]
+    rec = torch.empty((n, L, 2, nbytes), dtype=torch.uint8, pin_memory=True) if args.op != "copy_blocks" else None
+    stream = torch.cuda.current_stream()
+    sh = int(stream.cuda_stream)
+
+    def step(i):
+        if args.op == "copy_blocks":
+            pr = pair_sets[i & 1]
+            rc = lib.rllm_cache_copy_blocks(kt.data_ptr(), vt.data_ptr(), L, pr.data_ptr(), n, nb, nbytes, sh)
+        else:
+            ids = id_sets[i & 1]
+            fn = lib.rllm_cache_swap_out if args.op == "swap_out" else lib.rllm_cache_swap_in
+            rc = fn(kt.data_ptr(), vt.data_ptr(), L, ids.data_ptr(), n, nb, nbytes, None, n, rec.data_ptr(), sh)
+        if rc:
+            raise rllm_amd.KernelError(rc, args.op)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = ev0.elapsed_time(ev1) / args.steps
+    moved = n * L * 2 * nbytes            # bytes of the blocks moved
+    nbytes_rw = 2 * moved                 # each read once and written once
+    achieved = nbytes_rw / (kernel_ms * 1e-3) / 1e9
+    res = {
+        "metric": f"{args.op} GB/s (bytes read + written)",
+        "value": round(nbytes_rw / (wall / args.steps) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "zero-filled caches (byte movement)",
+        "config": {"workload": w.name, "config_index": w.index, "op": args.op, "blocks_per_step": n,
+                   "layers": L, "block_bytes": nbytes, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm" if args.op == "copy_blocks" else "host link", "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBS if args.op == "copy_blocks" else None, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4) if args.op == "copy_blocks" else None,
+                     "traffic": None, "kernel_ms": round(kernel_ms, 5), "algorithmic_bytes": nbytes_rw},
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def workloads_host(w):
     from rllm_amd import workloads
     return workloads.host_tensors(w)
@@ -253,9 +326,11 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
                     help="BASELINE config: 2 (default) is the headline decode line; 5 is chunked prefill")
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
-    ap.add_argument("--op", default="attention", choices=["attention", "rope_cache"],
+    ap.add_argument("--op", default="attention",
+                    choices=["attention", "rope_cache", "copy_blocks", "swap_out", "swap_in"],
                     help="attention (default): the config's decode or prefill line; rope_cache: the fused "
-                         "RoPE + cache write over the config's new tokens")
+                         "RoPE + cache write over the config's new tokens; copy_blocks / swap_out / swap_in: "
+                         "block-list moves over a 32-layer cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
@@ -277,6 +352,8 @@ def main() -> int:
     w = workloads.config(args.config)
     if args.op == "rope_cache":
         return bench_rope_cache(args, w, lib, dev)
+    if args.op in ("copy_blocks", "swap_out", "swap_in"):
+        return bench_block_moves(args, w, lib, dev)
     if args.config == 5:
         return bench_prefill(args, w, lib, dev)
     fp8 = w.kv_dtype.startswith("fp8")

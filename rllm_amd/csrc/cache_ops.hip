@@ -228,7 +228,7 @@ inline unsigned fill_grid(int64_t n16) {
 // ---------------------------------------------------------------------------
 // batched block copy (copy-on-write) and swap to / from pinned host records
 // ---------------------------------------------------------------------------
-// One workgroup per (pair or id, layer): 16-byte accesses when the block and
+// One workgroup per (pair, layer, K or V) or (id, layer): 16-byte accesses when the block and
 // both bases are 16-byte aligned (uniform per workgroup), bytes otherwise; 4
 // independent 16-byte loads in flight per lane.
 __device__ __forceinline__ void copy_bytes(const uint8_t* __restrict__ s, uint8_t* __restrict__ d,
@@ -252,8 +252,8 @@ __device__ __forceinline__ void copy_bytes(const uint8_t* __restrict__ s, uint8_
     }
 }
 
-// pairs[2p] -> pairs[2p + 1] in every layer's key and value cache; pairs with
-// a block outside [0, num_blocks) or src == dst are skipped
+// pairs[2p] -> pairs[2p + 1] in every layer's key (z = 0) and value (z = 1)
+// cache; pairs with a block outside [0, num_blocks) or src == dst are skipped
 __global__ __launch_bounds__(256) void copy_blocks_kernel(const uint64_t* __restrict__ key_caches,
                                                           const uint64_t* __restrict__ value_caches,
                                                           const int64_t* __restrict__ pairs,
@@ -262,10 +262,8 @@ __global__ __launch_bounds__(256) void copy_blocks_kernel(const uint64_t* __rest
     const int32_t layer = blockIdx.y;
     const int64_t src = pairs[2 * p], dst = pairs[2 * p + 1];
     if (src < 0 || dst < 0 || src >= num_blocks || dst >= num_blocks || src == dst) return;
-    for (int kv = 0; kv < 2; ++kv) {
-        uint8_t* base = reinterpret_cast<uint8_t*>(kv ? value_caches[layer] : key_caches[layer]);
-        copy_bytes(base + src * block_nbytes, base + dst * block_nbytes, block_nbytes);
-    }
+    uint8_t* base = reinterpret_cast<uint8_t*>(blockIdx.z ? value_caches[layer] : key_caches[layer]);
+    copy_bytes(base + src * block_nbytes, base + dst * block_nbytes, block_nbytes);
 }
 
 // record r of `host` = [layer][K, V][block_nbytes]; id i uses record
@@ -419,7 +417,8 @@ int32_t rllm_cache_copy_blocks(const uint64_t* key_caches, const uint64_t* value
     const int32_t rc = check_block_lists(key_caches, value_caches, block_pairs, num_pairs, num_layers, num_blocks,
                                          block_nbytes);
     if (rc) return rc;
-    hipLaunchKernelGGL(copy_blocks_kernel, dim3(static_cast<unsigned>(num_pairs), static_cast<unsigned>(num_layers)),
+    hipLaunchKernelGGL(copy_blocks_kernel,
+                       dim3(static_cast<unsigned>(num_pairs), static_cast<unsigned>(num_layers), 2u),
                        dim3(256), 0, as_stream(stream), key_caches, value_caches, block_pairs, num_blocks,
                        block_nbytes);
     return launch_status();
