@@ -313,6 +313,72 @@ def bench_block_moves(args, w, lib, dev) -> int:
     return 0
 
 
+def bench_fused(args, w, lib, dev) -> int:
+    """--op rmsnorm / silu_mul at Llama-3-8B widths (hidden 4096, MLP 14336)
+    over the config's step tokens (config 5: 4096 prefill tokens).  Bytes:
+    RMSNorm reads x and writes y (the weight row stays in L2); SiLU-mul reads
+    gate and up and writes the product."""
+    import numpy as np
+    import torch
+
+    import rllm_amd
+    T = max(w.num_tokens, 1)
+    hidden, inter = 4096, 14336
+    g = torch.Generator(device="cpu").manual_seed(w.index)
+    stream = torch.cuda.current_stream()
+    sh = int(stream.cuda_stream)
+    if args.op == "rmsnorm":
+        sets = [torch.randn(T, hidden, generator=g).bfloat16().to(dev) for _ in range(4)]
+        wgt = (1 + 0.1 * torch.randn(hidden, generator=g)).bfloat16().to(dev)
+        outs = [torch.empty_like(x) for x in sets]
+        nbytes = 2 * T * hidden * 2
+
+        def step(i):
+            rc = lib.rllm_rmsnorm_ex(outs[i & 3].data_ptr(), sets[i & 3].data_ptr(), wgt.data_ptr(), hidden,
+                                     T * hidden, 1e-5, rllm_amd.DTYPE_BF16, sh)
+            if rc:
+                raise rllm_amd.KernelError(rc, "rllm_rmsnorm_ex")
+    else:
+        sets = [(torch.randn(T, inter, generator=g).bfloat16().to(dev),
+                 torch.randn(T, inter, generator=g).bfloat16().to(dev)) for _ in range(2)]
+        outs = [torch.empty_like(a) for a, _ in sets]
+        nbytes = 3 * T * inter * 2
+
+        def step(i):
+            a, b = sets[i & 1]
+            rc = lib.rllm_silu_mul_ex(outs[i & 1].data_ptr(), a.data_ptr(), b.data_ptr(), T * inter,
+                                      rllm_amd.DTYPE_BF16, sh)
+            if rc:
+                raise rllm_amd.KernelError(rc, "rllm_silu_mul_ex")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = ev0.elapsed_time(ev1) / args.steps
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    res = {
+        "metric": f"{args.op} GB/s (algorithmic bytes)", "value": round(nbytes / (wall / args.steps) / 1e9, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1) (seeded)",
+        "config": {"workload": w.name, "config_index": w.index, "op": args.op, "tokens": T,
+                   "width": hidden if args.op == "rmsnorm" else inter, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel_ms": round(kernel_ms, 5),
+                     "algorithmic_bytes": nbytes},
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def workloads_host(w):
     from rllm_amd import workloads
     return workloads.host_tensors(w)
@@ -327,10 +393,11 @@ def main() -> int:
                     help="BASELINE config: 2 (default) is the headline decode line; 5 is chunked prefill")
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
     ap.add_argument("--op", default="attention",
-                    choices=["attention", "rope_cache", "copy_blocks", "swap_out", "swap_in"],
+                    choices=["attention", "rope_cache", "copy_blocks", "swap_out", "swap_in", "rmsnorm",
+                             "silu_mul"],
                     help="attention (default): the config's decode or prefill line; rope_cache: the fused "
                          "RoPE + cache write over the config's new tokens; copy_blocks / swap_out / swap_in: "
-                         "block-list moves over a 32-layer cache")
+                         "block-list moves over a 32-layer cache; rmsnorm / silu_mul: at Llama-3-8B widths")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
@@ -354,6 +421,8 @@ def main() -> int:
         return bench_rope_cache(args, w, lib, dev)
     if args.op in ("copy_blocks", "swap_out", "swap_in"):
         return bench_block_moves(args, w, lib, dev)
+    if args.op in ("rmsnorm", "silu_mul"):
+        return bench_fused(args, w, lib, dev)
     if args.config == 5:
         return bench_prefill(args, w, lib, dev)
     fp8 = w.kv_dtype.startswith("fp8")

@@ -316,6 +316,30 @@ int32_t rllm_rope_cache_write(void *q_out, const void *q, const void *k, const v
 int32_t rllm_rope_tables(float *cos_cache, float *sin_cache, int64_t max_position,
                          int64_t head_dim, float theta);
 
+/* Replace rllm_fused_rmsnorm_f16(_sync) and rllm_fused_silu_mul_f16(_sync),
+ * fused.cu:20-166; bound at fused.rs:18-51.  They compute the model's ops
+ * rather than fused.cu's kernels (whose RMSNorm reduces per CUDA block, wrong
+ * for rows longer than one block):
+ *   RMSNorm  (layers.rs:128-140): per row of hidden_size elements,
+ *            y = x / sqrt(mean(x^2) + eps) * weight in f32, rounded to the dtype
+ *   SiLU-mul (layers.rs:214-220): out = silu(gate) * up in the dtype, silu(x)
+ *            = x / (1 + exp(-x)) with each op rounded to the dtype
+ * n_elements must be a multiple of hidden_size, hidden_size a multiple of 8
+ * and the RMSNorm pointers 16-byte aligned (hipErrorInvalidValue otherwise). */
+int32_t rllm_fused_rmsnorm_f16(uint16_t *output, const uint16_t *input, const uint16_t *weight,
+                               int64_t hidden_size, int64_t n_elements, float eps, uintptr_t stream);
+int32_t rllm_fused_rmsnorm_f16_sync(uint16_t *output, const uint16_t *input, const uint16_t *weight,
+                                    int64_t hidden_size, int64_t n_elements, float eps);
+int32_t rllm_fused_silu_mul_f16(uint16_t *output, const uint16_t *gate, const uint16_t *up,
+                                int64_t n_elements, uintptr_t stream);
+int32_t rllm_fused_silu_mul_f16_sync(uint16_t *output, const uint16_t *gate, const uint16_t *up,
+                                     int64_t n_elements);
+/* New: the same for dtype RLLM_DTYPE_F16 or RLLM_DTYPE_BF16. */
+int32_t rllm_rmsnorm_ex(void *output, const void *input, const void *weight, int64_t hidden_size,
+                        int64_t n_elements, float eps, int32_t dtype, uintptr_t stream);
+int32_t rllm_silu_mul_ex(void *output, const void *gate, const void *up, int64_t n_elements,
+                         int32_t dtype, uintptr_t stream);
+
 /* Replaces rllm_cache_block_copy(_sync), cache_ops.cu:264-292; bound at
  * cache_ops.rs:80-94. */
 int32_t rllm_cache_block_copy(const uint8_t *src, uint8_t *dst, int64_t block_nbytes,

@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
     L.orc_slot_mapping.argtypes = [P, i64, P, i64, i64, P]
     L.orc_cache_write.argtypes = [P, P, P, P, P, i64, i64, i64, i64, i64, c.c_int, c.c_int,
                                   c.c_float, c.c_float]
+    L.orc_rmsnorm.argtypes = [P, P, P, i64, i64, c.c_float, c.c_int]
+    L.orc_silu_mul.argtypes = [P, P, P, i64, c.c_int]
     L.orc_copy_blocks.argtypes = [P, P, i64, P, i64, i64, i64]
     L.orc_swap_blocks.argtypes = [P, P, i64, P, i64, P, i64, i64, i64, P, c.c_int]
     L.orc_rope_cache_build.argtypes = [P, P, i64, i64, c.c_float]
@@ -130,6 +132,23 @@ def cache_write(key_cache, value_cache, new_key, new_value, slot_mapping, block_
     lib().orc_cache_write(_p(key_cache), _p(value_cache), _p(np.ascontiguousarray(new_key)),
                           _p(np.ascontiguousarray(new_value)), _p(sm), sm.size, hkv, d, bs, nb,
                           in_kind, cache_kind, k_scale, v_scale)
+
+
+def rmsnorm(x, weight, eps: float, kind: int):
+    """x: 16-bit bits [rows, hidden]; weight [hidden]; returns bits."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(weight, dtype=np.uint16)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(_p(out), _p(x), _p(w), x.shape[0], x.shape[1], eps, kind)
+    return out
+
+
+def silu_mul(gate, up, kind: int):
+    g = np.ascontiguousarray(gate, dtype=np.uint16)
+    u = np.ascontiguousarray(up, dtype=np.uint16)
+    out = np.empty_like(g)
+    lib().orc_silu_mul(_p(out), _p(g), _p(u), g.size, kind)
+    return out
 
 
 def _ptr_array(arrays):

@@ -295,6 +295,54 @@ void orc_cache_write(void *key_cache, void *value_cache, const void *new_key,
     }
 }
 
+static inline float r16(float x, int kind) {
+    return kind == ORC_BF16 ? orc_bf16_to_f32(orc_f32_to_bf16(x)) : orc_f16_to_f32(orc_f32_to_f16(x));
+}
+
+/* ------------------------------------------------------------------ */
+/* RMSNorm and SiLU-mul                                                 */
+/* ------------------------------------------------------------------ */
+
+/* RmsNorm::forward (layers.rs:128-140) with Candle 0.9.2's op sequence: x in
+ * f32, sum of squares (sequential f32), mean = sum * f32(1/H) (Candle's mean
+ * scales the sum), variance = mean + f32(eps), y = (x / sqrt(variance)) * w,
+ * rounded to the dtype. */
+void orc_rmsnorm(uint16_t *out, const uint16_t *in, const uint16_t *weight, int64_t rows,
+                 int64_t hidden, float eps, int kind) {
+    const float inv = (float)(1.0 / (double)hidden);
+    for (int64_t r = 0; r < rows; r++) {
+        const uint16_t *x = in + r * hidden;
+        float ss = 0.f;
+        for (int64_t i = 0; i < hidden; i++) {
+            float v = decode_elem(x, kind, i);
+            float sq = v * v;
+            ss += sq;
+        }
+        float mean = ss * inv;
+        float var = mean + eps;
+        float sd = sqrtf(var);
+        for (int64_t i = 0; i < hidden; i++) {
+            float q = decode_elem(x, kind, i) / sd;
+            float y = q * decode_elem(weight, kind, i);
+            out[r * hidden + i] = kind == ORC_BF16 ? orc_f32_to_bf16(y) : orc_f32_to_f16(y);
+        }
+    }
+}
+
+/* silu(gate) * up in the dtype (layers.rs:214-220): Candle 0.9.2's silu is
+ * x / (1 + exp(-x)) with every op rounded to the dtype, then the product is
+ * rounded.  exp is libm expf. */
+void orc_silu_mul(uint16_t *out, const uint16_t *gate, const uint16_t *up, int64_t n, int kind) {
+    for (int64_t i = 0; i < n; i++) {
+        float g = decode_elem(gate, kind, i), u = decode_elem(up, kind, i);
+        float e = r16(expf(-g), kind);
+        float d = r16(1.0f + e, kind);
+        float sv = r16(g / d, kind);
+        float y = sv * u;
+        out[i] = kind == ORC_BF16 ? orc_f32_to_bf16(y) : orc_f32_to_f16(y);
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* block copy (copy-on-write) and swap records                          */
 /* ------------------------------------------------------------------ */
@@ -357,10 +405,6 @@ void orc_rope_cache_build(float *cos_cache, float *sin_cache, int64_t max_positi
             sin_cache[p * half + j] = (float)sin(ang);
         }
     }
-}
-
-static inline float r16(float x, int kind) {
-    return kind == ORC_BF16 ? orc_bf16_to_f32(orc_f32_to_bf16(x)) : orc_f16_to_f32(orc_f32_to_f16(x));
 }
 
 /* apply_rotary_emb (rope.rs:57-82) in the activation dtype: cos and sin are

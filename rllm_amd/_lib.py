@@ -69,6 +69,12 @@ SIGNATURES = {
     "rllm_cache_copy_blocks": [_P, _P, _I64, _P, _I64, _I64, _I64, _U],
     "rllm_cache_swap_out": [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _U],
     "rllm_cache_swap_in": [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _U],
+    "rllm_fused_rmsnorm_f16": [_P, _P, _P, _I64, _I64, _F, _U],
+    "rllm_fused_rmsnorm_f16_sync": [_P, _P, _P, _I64, _I64, _F],
+    "rllm_fused_silu_mul_f16": [_P, _P, _P, _I64, _U],
+    "rllm_fused_silu_mul_f16_sync": [_P, _P, _P, _I64],
+    "rllm_rmsnorm_ex": [_P, _P, _P, _I64, _I64, _F, _I32, _U],
+    "rllm_silu_mul_ex": [_P, _P, _P, _I64, _I32, _U],
     "rllm_cache_block_copy": [_P, _P, _I64, _I64, _U],
     "rllm_cache_block_copy_sync": [_P, _P, _I64, _I64],
     "rllm_cache_zero": [_P, _I64, _U],
