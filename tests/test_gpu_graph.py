@@ -127,3 +127,70 @@ def test_prefill_graph_replays_match_eager(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(static_out, eager), f"replay {r} differs from the eager call"
+
+
+def test_full_decode_step_graph_with_rope_and_fused_ops(dev):
+    # a whole layer's decode-path kernels in one graph: RMSNorm of the hidden
+    # state, fused RoPE + cache write (q rotated in place), decode attention,
+    # SiLU-mul; replays match eager bit for bit, with eager work in between
+    x = _decode_inputs(dev, 97)
+    B, hq, D = x["q"].shape
+    hkv = x["kc"].shape[1]
+    pos = (x["sl"] - 1).to(torch.int32)
+    cos, sin = ops.rope_cache_tables(4096, D, 500000.0, device=dev)
+    ws = torch.zeros(max(A.decode_workspace_size(B, hq, hkv, D, 16, x["bt"].shape[1], 0), 1),
+                     dtype=torch.uint8, device=dev)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    hidden = torch.randn(B, 4096, generator=g).bfloat16().to(dev)
+    wn = (1 + 0.1 * torch.randn(4096, generator=g)).bfloat16().to(dev)
+    gate = torch.randn(B, 14336, generator=g).bfloat16().to(dev)
+    up = torch.randn(B, 14336, generator=g).bfloat16().to(dev)
+    q0 = x["q"].clone()
+    kc0, vc0 = x["kc"].clone(), x["vc"].clone()
+
+    def step(out, qbuf, normed, act):
+        ops.rmsnorm(hidden, wn, 1e-5, out=normed)
+        qbuf.copy_(q0)
+        ops.rope_and_cache(qbuf, x["nk"], x["nv"], x["kc"], x["vc"], x["slots"], pos, cos, sin, q_out=qbuf)
+        ops.paged_decode(qbuf, x["kc"], x["vc"], x["bt"], x["sl"], x["scale"], out=out, workspace=ws,
+                         validate=False)
+        ops.silu_mul(gate, up, out=act)
+
+    def fresh_cache():
+        x["kc"].copy_(kc0)
+        x["vc"].copy_(vc0)
+
+    bufs = lambda: (torch.empty_like(q0), torch.empty_like(q0), torch.empty_like(hidden), torch.empty_like(gate))
+    log_case("graph full decode step eager")
+    e_out, e_q, e_n, e_a = bufs()
+    fresh_cache()
+    step(e_out, e_q, e_n, e_a)
+    torch.cuda.synchronize()
+    e_kc = x["kc"].clone()
+
+    s_out, s_q, s_n, s_a = bufs()
+    gr = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(s_out, s_q, s_n, s_a)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(gr):
+        step(s_out, s_q, s_n, s_a)
+    torch.cuda.synchronize()
+    o_out, o_q, o_n, o_a = bufs()
+    for r in range(3):
+        for t in (s_out, s_q, s_n, s_a):
+            t.zero_()
+        fresh_cache()
+        log_case(f"graph full decode step replay {r}")
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(s_out, e_out) and torch.equal(s_q, e_q), f"replay {r}: attention differs"
+        assert torch.equal(s_n, e_n) and torch.equal(s_a, e_a), f"replay {r}: fused ops differ"
+        assert torch.equal(x["kc"], e_kc), f"replay {r}: key cache differs"
+        fresh_cache()
+        step(o_out, o_q, o_n, o_a)            # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(o_out, e_out)
