@@ -95,12 +95,29 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* __restrict__ out
     // Candle: mean = sum * (1/H), variance = mean * 1 + eps, then x / sqrt(variance)
     const float var = ss * inv_hidden + eps;
     const float r = __builtin_sqrtf(var);
+    // x / r correctly rounded without a division per element (Markstein's
+    // theorem): yr = RN(1/r) once per row, q = RN(x * yr) is within one ulp,
+    // the residual x - q*r is exact with an FMA, and RN(q + residual * yr) is
+    // the correctly rounded quotient when nothing underflows or overflows.
+    // Zero, tiny (< 2^-100), infinite and NaN x, and a row whose r or 1/r is
+    // not a normal number, take the division.
+    const float yr = 1.0f / r;
+    const bool row_ok = __builtin_isnormal(r) && __builtin_isnormal(yr);
+    auto quotient = [&](float xv) -> float {
+        const float ax = __builtin_fabsf(xv);
+        if (row_ok && ax >= 0x1p-100f && ax <= 0x1p100f) {
+            const float q = xv * yr;
+            const float rem = __builtin_fmaf(-q, r, xv);
+            return __builtin_fmaf(rem, yr, q);
+        }
+        return xv / r;
+    };
     auto scale_chunk = [&](const uint4 xv, int32_t ch) {
         uint16_t e[8], w[8], o[8];
         split8(xv, e);
         split8(reinterpret_cast<const uint4*>(weight)[ch], w);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = st16<KIND>((ld16<KIND>(e[i]) / r) * ld16<KIND>(w[i]));
+        for (int i = 0; i < 8; ++i) o[i] = st16<KIND>(quotient(ld16<KIND>(e[i])) * ld16<KIND>(w[i]));
         reinterpret_cast<uint4*>(y)[ch] = join8(o);
     };
     if constexpr (CPL > 0) {

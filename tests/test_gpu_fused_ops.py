@@ -41,6 +41,21 @@ def test_rmsnorm_matches_oracle(dev, kind, rows, hidden):
     _ulp_check(bits16(y), O.rmsnorm(x, w, 1e-5, kind), f"rmsnorm {rows}x{hidden}")
 
 
+@pytest.mark.parametrize("kind", [O.BF16, O.F16])
+def test_rmsnorm_bit_exact_when_sums_are_exact(dev, kind):
+    # x = k/8 (|k| <= 64): every square and every partial sum is exact in f32,
+    # so the summation order cannot matter and the GPU must give the oracle's
+    # bytes exactly (this pins the per-element quotient x / sqrt(var))
+    rng = np.random.default_rng(17)
+    rows, hidden = 512, 4096
+    x = O.encode((rng.integers(-64, 65, (rows, hidden)) / 8).astype(np.float32), kind)
+    w = O.encode((1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32), kind)
+    log_case(f"rmsnorm exact sums kind={kind}")
+    y = bits16(ops.rmsnorm(t16(x, DT[kind], dev), t16(w, DT[kind], dev), 1e-5))
+    want = O.rmsnorm(x, w, 1e-5, kind)
+    assert np.array_equal(y, want), f"{int((y != want).sum())} of {y.size} differ"
+
+
 def test_rmsnorm_reference_symbol_known_answer(dev):
     # fused.rs:512-567 through rllm_fused_rmsnorm_f16_sync
     x = O.encode(np.array([1, 2, 3, 4, 2, 4, 6, 8], np.float32), O.F16)
