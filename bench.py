@@ -1,7 +1,7 @@
 """Benchmark of the gfx950 paged-attention decode path (one GPU).
 
 A "step" is one decode paged-attention call (one attention layer) over the
-BASELINE config-2 batch: Llama-3-8B layer shape, 64 sequences, 32 q heads /
+benchmark config-2 batch: Llama-3-8B layer shape, 64 sequences, 32 q heads /
 8 kv heads, head_dim 128, block size 16, contexts uniform in [128, 4096],
 bf16 KV N(0,1), block tables randomly permuted over a pool sized for the sum of
 contexts + 10% free blocks.  Inputs are resident in HBM before timing.  Steps
@@ -390,7 +390,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
-                    help="BASELINE config: 2 (default) is the headline decode line; 5 is chunked prefill")
+                    help="benchmark config: 2 (default) is the headline decode line; 5 is chunked prefill")
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
     ap.add_argument("--op", default="attention",
                     choices=["attention", "rope_cache", "copy_blocks", "swap_out", "swap_in", "rmsnorm",
@@ -405,7 +405,7 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the decode path "
-              "shards by sequence / kv head with no exchange, see DESIGN.md", file=sys.stderr)
+              "would shard by sequence / kv head with no exchange between GPUs", file=sys.stderr)
         return 2
 
     import numpy as np

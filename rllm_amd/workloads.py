@@ -122,7 +122,7 @@ def _tables_from_pool(rng, nblks, pool, max_blocks):
 
 
 def config(index: int) -> Workload:
-    """BASELINE configuration `index` (1-based; 4 = prefix-aliased 4a, 6 = split-K 4b)."""
+    """Benchmark configuration `index` (1-based; 4 = prefix-aliased 4a, 6 = split-K 4b)."""
     rng = _rng(index)
     if index == 1:
         B, ctx = 8, 512

@@ -144,7 +144,7 @@ def test_decode_reference_symbols(dev):
 
 
 def test_decode_bf16_symbol_config1_full(dev):
-    """BASELINE config 1 at full size through rllm_paged_attention_decode_bf16."""
+    """Benchmark config 1 at full size through rllm_paged_attention_decode_bf16."""
     w = workloads.config(1)
     qb, kb, vb = workloads.host_tensors(w)
     ref = oracle_ref(qb, O.BF16, kb, vb, O.BF16, w.block_tables, w.seq_lens, w.scale)
@@ -160,7 +160,7 @@ def test_decode_bf16_symbol_config1_full(dev):
 
 
 def test_decode_config2_full_and_split_equivalence(dev):
-    """BASELINE config 2 (B=64, ctx U[128,4096]) at full size vs the oracle, and
+    """Benchmark config 2 (B=64, ctx U[128,4096]) at full size vs the oracle, and
     every partition size (split-K) against single pass."""
     w = workloads.config(2)
     qb, kb, vb = workloads.host_tensors(w)
@@ -177,7 +177,7 @@ def test_decode_config2_full_and_split_equivalence(dev):
 
 
 def test_decode_prefix_aliased_equals_oracle(dev):
-    """BASELINE config 4a layout (every table aliases one 64-block prefix), reduced batch."""
+    """Benchmark config 4a layout (every table aliases one 64-block prefix), reduced batch."""
     w = workloads.config(4)
     qb, kb, vb = workloads.host_tensors(w)
     sel = slice(0, 16)

@@ -147,7 +147,7 @@ def test_prefill_reference_symbols(dev):
 
 
 def test_prefill_config5_full_against_decode_kernel(dev):
-    """BASELINE config 5 at full size (8 x 512 new tokens over 2048 cached).
+    """Benchmark config 5 at full size (8 x 512 new tokens over 2048 cached).
     Size-independent check: the last new token of every sequence attends the
     whole context, so its prefill row must equal a decode at ctx = seq_len (a
     different kernel); the first new token equals a decode at ctx = cached + 1.
