@@ -386,6 +386,30 @@ int32_t rllm_cache_swap_in(const uint64_t *key_caches, const uint64_t *value_cac
                            int64_t num_blocks, int64_t block_nbytes, const int64_t *record_slots,
                            int64_t num_records, const void *host_records, uintptr_t stream);
 
+/* Replace rllm_vector_add_f32(_sync) and rllm_block_copy(_sync),
+ * smoke.cu:21-66; bound at cuda.rs:17-35.  out = a + b (f32); nbytes
+ * contiguous bytes src -> dst. */
+int32_t rllm_vector_add_f32(const float *a, const float *b, float *out, int64_t n, uintptr_t stream);
+int32_t rllm_vector_add_f32_sync(const float *a, const float *b, float *out, int64_t n);
+int32_t rllm_block_copy(const uint8_t *src, uint8_t *dst, int64_t nbytes, uintptr_t stream);
+int32_t rllm_block_copy_sync(const uint8_t *src, uint8_t *dst, int64_t nbytes);
+
+/* Replace rllm_fused_rope_f16(_sync), fused.cu:168-256; bound at fused.rs:54-76.
+ * The kernel's own convention, kept for its callers: interleaved pairs
+ * (2i, 2i+1), freq = 1 / theta^(2i / head_dim), angle = position * freq, cos /
+ * sin in f32 on the device, f16 in and out; q [num_tokens, Hq, D] -> out_q,
+ * k [num_tokens, Hkv, D] -> out_k (every kv head, also when Hkv > Hq, where
+ * the reference leaves heads unwritten).  The model's rotate-half RoPE is
+ * rllm_rope_cache_write. */
+int32_t rllm_fused_rope_f16(uint16_t *out_q, uint16_t *out_k, const uint16_t *query,
+                            const uint16_t *key, const int32_t *positions, int64_t num_tokens,
+                            int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                            float rope_theta, uintptr_t stream);
+int32_t rllm_fused_rope_f16_sync(uint16_t *out_q, uint16_t *out_k, const uint16_t *query,
+                                 const uint16_t *key, const int32_t *positions, int64_t num_tokens,
+                                 int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                 float rope_theta);
+
 /* Replace rllm_gpu_alloc / _free / _alloc_host / _free_host,
  * cache_ops.cu:417-439; bound at cache_ops.rs:100-103. */
 int32_t rllm_gpu_alloc(void **ptr, int64_t nbytes);

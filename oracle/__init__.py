@@ -61,6 +61,7 @@ def lib() -> ctypes.CDLL:
     L.orc_slot_mapping.argtypes = [P, i64, P, i64, i64, P]
     L.orc_cache_write.argtypes = [P, P, P, P, P, i64, i64, i64, i64, i64, c.c_int, c.c_int,
                                   c.c_float, c.c_float]
+    L.orc_rope_interleaved.argtypes = [P, P, P, i64, i64, i64, c.c_float]
     L.orc_rmsnorm.argtypes = [P, P, P, i64, i64, c.c_float, c.c_int]
     L.orc_silu_mul.argtypes = [P, P, P, i64, c.c_int]
     L.orc_copy_blocks.argtypes = [P, P, i64, P, i64, i64, i64]
@@ -132,6 +133,15 @@ def cache_write(key_cache, value_cache, new_key, new_value, slot_mapping, block_
     lib().orc_cache_write(_p(key_cache), _p(value_cache), _p(np.ascontiguousarray(new_key)),
                           _p(np.ascontiguousarray(new_value)), _p(sm), sm.size, hkv, d, bs, nb,
                           in_kind, cache_kind, k_scale, v_scale)
+
+
+def rope_interleaved(x, positions, theta: float):
+    """x: f16 bits [T, H, D]; the reference kernel's interleaved rotation."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    out = np.empty_like(x)
+    lib().orc_rope_interleaved(_p(out), _p(x), _p(pos), x.shape[0], x.shape[1], x.shape[2], theta)
+    return out
 
 
 def rmsnorm(x, weight, eps: float, kind: int):

@@ -343,6 +343,28 @@ void orc_silu_mul(uint16_t *out, const uint16_t *gate, const uint16_t *up, int64
     }
 }
 
+/* rllm_fused_rope_f16 (fused.cu:168-256): interleaved pairs, freq =
+ * 1 / powf(theta, 2i / D), angle = pos * freq, f32 cosf / sinf, f16 output of
+ * e*c - o*s and o*c + e*s (each product and the sum rounded in f32). */
+void orc_rope_interleaved(uint16_t *out, const uint16_t *x, const int32_t *positions,
+                          int64_t num_tokens, int64_t num_heads, int64_t head_dim, float theta) {
+    for (int64_t t = 0; t < num_tokens; t++) {
+        const float pos = (float)positions[t];
+        for (int64_t h = 0; h < num_heads; h++) {
+            const int64_t base = (t * num_heads + h) * head_dim;
+            for (int64_t i = 0; i < head_dim / 2; i++) {
+                const float freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+                const float ang = pos * freq;
+                const float c = cosf(ang), s = sinf(ang);
+                const float e = orc_f16_to_f32(x[base + 2 * i]), o = orc_f16_to_f32(x[base + 2 * i + 1]);
+                const float ec = e * c, os = o * s, oc = o * c, es = e * s;
+                out[base + 2 * i] = orc_f32_to_f16(ec - os);
+                out[base + 2 * i + 1] = orc_f32_to_f16(oc + es);
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* block copy (copy-on-write) and swap records                          */
 /* ------------------------------------------------------------------ */

@@ -101,6 +101,11 @@ void orc_rmsnorm(uint16_t *out, const uint16_t *in, const uint16_t *weight, int6
                  int64_t hidden, float eps, int kind);
 void orc_silu_mul(uint16_t *out, const uint16_t *gate, const uint16_t *up, int64_t n, int kind);
 
+/* ---- rllm_fused_rope_f16's interleaved rotation (fused.cu:168-256), applied
+ * to one tensor [num_tokens, num_heads, head_dim] of f16 bits. */
+void orc_rope_interleaved(uint16_t *out, const uint16_t *x, const int32_t *positions,
+                          int64_t num_tokens, int64_t num_heads, int64_t head_dim, float theta);
+
 /* ---- block copy and swap records ------------------------------------------
  * Per-layer block copies of a (src, dst) pair list (cache_ops.cu:252-262 for
  * the copy-on-write caller of block_pool.rs:286-302) and CpuKvOffloadStore

@@ -75,6 +75,12 @@ SIGNATURES = {
     "rllm_fused_silu_mul_f16_sync": [_P, _P, _P, _I64],
     "rllm_rmsnorm_ex": [_P, _P, _P, _I64, _I64, _F, _I32, _U],
     "rllm_silu_mul_ex": [_P, _P, _P, _I64, _I32, _U],
+    "rllm_vector_add_f32": [_P, _P, _P, _I64, _U],
+    "rllm_vector_add_f32_sync": [_P, _P, _P, _I64],
+    "rllm_block_copy": [_P, _P, _I64, _U],
+    "rllm_block_copy_sync": [_P, _P, _I64],
+    "rllm_fused_rope_f16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _U],
+    "rllm_fused_rope_f16_sync": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F],
     "rllm_cache_block_copy": [_P, _P, _I64, _I64, _U],
     "rllm_cache_block_copy_sync": [_P, _P, _I64, _I64],
     "rllm_cache_zero": [_P, _I64, _U],

@@ -95,3 +95,21 @@ def test_silu_mul_closed_forms(kind):
     # a dropped minus sign (silu(x) = x / (1 + exp(x))) is far outside it
     wrong = gd / (1 + np.exp(gd)) * ud
     assert np.mean(np.abs(got - wrong) > 5 * u * np.abs(want) + slack) > 0.5
+
+
+def test_interleaved_rope_reference_answers():
+    # fused.rs:569-650: q = [1, 0, 1, 0] at positions 0 and 1, head_dim 4,
+    # theta 1e4: position 0 is the identity; at position 1 pair 0 turns by 1
+    # rad and pair 1 by 1e4^(-2/4) = 0.01 rad
+    q = O.encode(np.array([[[1, 0, 1, 0]], [[1, 0, 1, 0]]], np.float32), O.F16)
+    out = O.decode(O.rope_interleaved(q, np.array([0, 1], np.int32), 10000.0), O.F16).astype(np.float64)
+    assert np.array_equal(out[0, 0], [1, 0, 1, 0])
+    want = [math.cos(1), math.sin(1), math.cos(0.01), math.sin(0.01)]
+    assert np.all(np.abs(out[1, 0] - want) <= 2.0 ** -11 * np.abs(want) + 2.0 ** -24)
+    # pairs are (2i, 2i+1): a one-hot at 2i+1 moves to (-sin, cos) of pair i only
+    x = np.zeros((1, 1, 8), np.float32)
+    x[0, 0, 3] = 1.0
+    got = O.decode(O.rope_interleaved(O.encode(x, O.F16), np.array([7], np.int32), 10000.0), O.F16)[0, 0]
+    ang = 7 * 10000.0 ** (-2 / 8)
+    assert got[0] == 0 and got[1] == 0 and np.all(got[4:] == 0)
+    assert abs(got[2] + math.sin(ang)) < 1e-3 and abs(got[3] - math.cos(ang)) < 1e-3
