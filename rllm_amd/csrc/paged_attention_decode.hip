@@ -37,6 +37,7 @@
 // No MFMA: per GQA group the decode contraction is a matrix-vector product and
 // the kernel is bound by HBM bandwidth.
 #include "common.h"
+#include "generic_attention.h"
 #include "../../include/rllm_kernels.h"
 
 #include <cmath>
@@ -1182,14 +1183,16 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
     RLLM_CHECK_ARG(out && q && kc && vc && bt && seq_lens);
     RLLM_CHECK_ARG(hq > 0 && hkv > 0 && hq % hkv == 0);
     const int64_t G = hq / hkv;
-    RLLM_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 8);
-    RLLM_CHECK_ARG(d == 64 || d == 128);
-    RLLM_CHECK_ARG(bs == BS);
     RLLM_CHECK_ARG(maxb >= 0 && maxb <= (int64_t(1) << 24));
     RLLM_CHECK_ARG(num_seqs <= (int64_t(1) << 20) && hq <= 1024);
     RLLM_CHECK_ARG(q_dtype == KIND_F16 || q_dtype == KIND_BF16);
     RLLM_CHECK_ARG(kv_dtype == q_dtype || kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2);
     RLLM_CHECK_ARG(std::isfinite(scale) && std::isfinite(k_scale) && std::isfinite(v_scale));
+    // other head_dims, block sizes and GQA ratios: the shape-general kernel
+    // (no workspace; partition_size does not apply)
+    if (!specialised_shape(hq, hkv, d, bs))
+        return generic_attention(out, q, kc, vc, bt, seq_lens, nullptr, num_seqs, num_seqs, hq, hkv, d, bs, maxb,
+                                 scale, q_dtype, kv_dtype, k_scale, v_scale, as_stream(stream));
     Kernels kern;
     RLLM_CHECK_ARG(pick_kernels(q_dtype, kv_dtype, d, G, &kern));
 
@@ -1287,8 +1290,10 @@ int64_t rllm_paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num
                                                    int64_t max_num_blocks_per_seq,
                                                    int64_t partition_size) {
     if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads ||
-        (head_dim != 64 && head_dim != 128) || block_size != BS || max_num_blocks_per_seq < 0)
+        max_num_blocks_per_seq < 0 || head_dim < 1 || block_size < 1)
         return -1;
+    if (!specialised_shape(num_q_heads, num_kv_heads, head_dim, block_size))
+        return head_dim <= 1024 ? 0 : -1;   // the shape-general kernel needs no workspace
     if (partition_size == 0) {
         const int res = max_resident_waves();
         if (res <= 0) return -1;

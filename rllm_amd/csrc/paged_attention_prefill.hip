@@ -37,6 +37,7 @@
 //   grid      = Hkv x (query tiles), kv head fastest, so on an 8-XCD part all
 //               tiles of one kv head share one XCD's L2.
 #include "common.h"
+#include "generic_attention.h"
 #include "../../include/rllm_kernels.h"
 
 #include <cmath>
@@ -477,14 +478,15 @@ int32_t prefill_impl(void* out, const void* q, const void* kc, const void* vc, c
     RLLM_CHECK_ARG(num_seqs > 0 && out && q && kc && vc && bt && seq_lens && qsl);
     RLLM_CHECK_ARG(hq > 0 && hkv > 0 && hq % hkv == 0);
     const int64_t G = hq / hkv;
-    RLLM_CHECK_ARG(G == 1 || G == 2 || G == 4 || G == 8);
-    RLLM_CHECK_ARG(d == 64 || d == 128);
-    RLLM_CHECK_ARG(bs == PF_BS);
     RLLM_CHECK_ARG(maxb >= 0 && maxb <= (int64_t(1) << 24));
     RLLM_CHECK_ARG(num_seqs <= (int64_t(1) << 20) && hq <= 1024 && num_tokens <= (int64_t(1) << 26));
     RLLM_CHECK_ARG(q_dtype == KIND_F16 || q_dtype == KIND_BF16);
     RLLM_CHECK_ARG(kv_dtype == q_dtype || kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2);
     RLLM_CHECK_ARG(std::isfinite(scale) && std::isfinite(k_scale) && std::isfinite(v_scale));
+    // other head_dims, block sizes and GQA ratios: the shape-general kernel
+    if (!specialised_shape(hq, hkv, d, bs))
+        return generic_attention(out, q, kc, vc, bt, seq_lens, qsl, num_seqs, num_tokens, hq, hkv, d, bs, maxb,
+                                 scale, q_dtype, kv_dtype, k_scale, v_scale, as_stream(stream));
 
     PrefillArgs a{};
     a.out = out;

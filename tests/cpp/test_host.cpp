@@ -145,7 +145,7 @@ static void slot_mappings() {
 static void error_mapping() {
     uint16_t* p = reinterpret_cast<uint16_t*>(0x1000);   // never dereferenced: validation fails first
     const int32_t* ip = reinterpret_cast<const int32_t*>(0x1000);
-    auto r = paged_attention_decode_f16(p, p, p, p, ip, ip, 4, 32, 8, 96, 16, 4, 0.1f, 0);   // head_dim 96
+    auto r = paged_attention_decode_f16(p, p, p, p, ip, ip, 4, 32, 8, 2048, 16, 4, 0.1f, 0);   // head_dim > 1024
     CHECK(r.is_err() && r.error().kind == CudaKernelError::Kind::KernelError && r.error().code == 1);
     CHECK(r.error().message() == "GPU kernel returned error code 1");
     r = paged_attention_decode_f16(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 32, 8, 128, 16, 4,

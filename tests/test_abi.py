@@ -91,10 +91,12 @@ HIP_ERROR_INVALID_VALUE = 1
 def test_decode_rejects_unsupported_shapes_without_launch():
     L = rllm_amd.lib()
     P = 0x1000  # never dereferenced: validation fails first
-    # head_dim 96, block size 8, GQA ratio 3, non-divisible heads, null pointer
-    assert L.rllm_paged_attention_decode_bf16(P, P, P, P, P, P, 4, 32, 8, 96, 16, 4, 0.1, 0) == 1
-    assert L.rllm_paged_attention_decode_f16(P, P, P, P, P, P, 4, 32, 8, 128, 8, 4, 0.1, 0) == 1
-    assert L.rllm_paged_attention_decode_bf16(P, P, P, P, P, P, 4, 24, 8, 128, 16, 4, 0.1, 0) == 1
+    # head_dim above 1024, block size 0, no q heads, non-divisible heads, null
+    # pointer (other head_dims, block sizes and GQA ratios are computed by the
+    # shape-general kernel, so they are not rejected)
+    assert L.rllm_paged_attention_decode_bf16(P, P, P, P, P, P, 4, 32, 8, 2048, 16, 4, 0.1, 0) == 1
+    assert L.rllm_paged_attention_decode_f16(P, P, P, P, P, P, 4, 32, 8, 128, 0, 4, 0.1, 0) == 1
+    assert L.rllm_paged_attention_decode_bf16(P, P, P, P, P, P, 4, 0, 8, 128, 16, 4, 0.1, 0) == 1
     assert L.rllm_paged_attention_decode_bf16(P, P, P, P, P, P, 4, 30, 8, 128, 16, 4, 0.1, 0) == 1
     assert L.rllm_paged_attention_decode_bf16(0, P, P, P, P, P, 4, 32, 8, 128, 16, 4, 0.1, 0) == 1
     # bad dtype codes, partition size, too-small caller workspace
@@ -124,7 +126,8 @@ def test_empty_work_returns_zero_without_launch():
 def test_prefill_and_cache_write_reject_invalid():
     L = rllm_amd.lib()
     P = 0x1000
-    assert L.rllm_paged_attention_prefill_bf16(P, P, P, P, P, P, P, 2, 10, 32, 8, 80, 16, 4, 0.1, 0) == 1
+    assert L.rllm_paged_attention_prefill_bf16(P, P, P, P, P, P, P, 2, 10, 32, 8, 2048, 16, 4, 0.1, 0) == 1
+    assert L.rllm_paged_attention_prefill_bf16(P, P, P, P, P, P, P, 2, 10, 32, 6, 128, 16, 4, 0.1, 0) == 1
     assert L.rllm_paged_attention_prefill_ex(P, P, P, P, P, P, P, 2, 10, 32, 8, 128, 16, 4, 0.1,
                                              0, 1, 1.0, 1.0, 0) == 1
     assert L.rllm_cache_write_f16(0, 0, 0, 0, 0, 4, 8, 128, 16, 10, 0) == 1
@@ -142,7 +145,10 @@ def test_workspace_size_query():
     # 256 blocks = 4096 tokens in 512-token partitions: 8 partitions
     assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 128, 16, 256, 512) == \
         64 * 32 * 8 * (128 + 2) * 4
-    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 96, 16, 256, 512) == -1
+    # shapes of the shape-general kernel need none; head_dim above 1024 is invalid
+    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 96, 16, 256, 512) == 0
+    assert L.rllm_paged_attention_decode_workspace_size(64, 24, 8, 128, 32, 256, 0) == 0
+    assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 2048, 16, 256, 512) == -1
     assert L.rllm_paged_attention_decode_workspace_size(64, 32, 8, 128, 16, 256, 100) == -1
     assert L.rllm_paged_attention_decode_workspace_size(64, 30, 8, 128, 16, 256, 512) == -1
 
@@ -150,5 +156,5 @@ def test_workspace_size_query():
 def test_errors_surface_as_kernel_error():
     with pytest.raises(rllm_amd.KernelError) as ei:
         _lib.call("rllm_paged_attention_decode_bf16", 0x10, 0x10, 0x10, 0x10, 0x10, 0x10, 4, 32,
-                  8, 96, 16, 4, 0.1, 0)
+                  8, 2048, 16, 4, 0.1, 0)
     assert ei.value.code == HIP_ERROR_INVALID_VALUE
