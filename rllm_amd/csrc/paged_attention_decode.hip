@@ -197,6 +197,9 @@ __device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
 
 // inclusive prefix sum across the wave: DPP row shifts within each 16-lane
 // row, then the totals of the rows below through SGPRs
+// lane of the calling wave (stream-mode workgroups may hold several waves)
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63); }
+
 __device__ __forceinline__ int wave_scan(int v) {
     v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
     v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
@@ -205,7 +208,7 @@ __device__ __forceinline__ int wave_scan(int v) {
     const int r0 = __builtin_amdgcn_readlane(v, 15);
     const int r1 = r0 + __builtin_amdgcn_readlane(v, 31);
     const int r2 = r1 + __builtin_amdgcn_readlane(v, 47);
-    const int row = static_cast<int>(threadIdx.x) >> 4;
+    const int row = lane_id() >> 4;
     return v + (row == 0 ? 0 : row == 1 ? r0 : row == 2 ? r1 : r2);
 }
 
@@ -302,8 +305,8 @@ struct Attn {
     }
 
     // QK lane roles in a window of 2^lnb blocks
-    __device__ __forceinline__ static int q_block(int lnb) { return (threadIdx.x >> 1) & ((1 << lnb) - 1); }
-    __device__ __forceinline__ static int q_slice(int lnb) { return threadIdx.x >> (lnb + 1); }
+    __device__ __forceinline__ static int q_block(int lnb) { return (lane_id() >> 1) & ((1 << lnb) - 1); }
+    __device__ __forceinline__ static int q_slice(int lnb) { return lane_id() >> (lnb + 1); }
 
     // this lane's block-table entry of the window (QK layout), -1 if none;
     // every lane loads (an in-range entry) so the load is never skipped
@@ -321,7 +324,7 @@ struct Attn {
                              (static_cast<int64_t>(p.s) * a.num_q_heads + p.h * G) * NKS;
 #pragma unroll
         for (int k = 0; k < QW; ++k) {
-            const int i = static_cast<int>(threadIdx.x) + 64 * k;
+            const int i = lane_id() + 64 * k;
             qr[k] = (i < QN) ? qw[i] : 0u;
         }
     }
@@ -329,7 +332,7 @@ struct Attn {
     __device__ __forceinline__ static void store_q(const uint32_t* qr, QP& qp) {
 #pragma unroll
         for (int k = 0; k < QW; ++k) {
-            const int i = static_cast<int>(threadIdx.x) + 64 * k;
+            const int i = lane_id() + 64 * k;
             if (i < QN) qp[i % NKS][i / NKS] = qr[k];
         }
     }
@@ -356,7 +359,7 @@ struct Attn {
         const int pbk = kval ? pb : kw.fb;
         const int ds = q_slice(w.lnb);
         const int nks_w = NKS >> (5 - w.lnb);
-        const int64_t in_tile = (static_cast<int64_t>(2 * ds * nks_w) * BS + (threadIdx.x & 1) * 8) * EB;
+        const int64_t in_tile = (static_cast<int64_t>(2 * ds * nks_w) * BS + (lane_id() & 1) * 8) * EB;
         kw.krow = kw.any ? static_cast<const char*>(a.k_cache) +
                                (static_cast<int64_t>(pbk) * a.num_kv_heads + h) * TILE * EB + in_tile
                          : reinterpret_cast<const char*>(g_empty_tile) + in_tile;
@@ -391,7 +394,7 @@ struct Attn {
     __device__ __forceinline__ static void attend(const DecodeArgs& a, int h, int ctx, const Win& w,
                                                   const KWin& kw, const QP& qp_lds, PL& p_lds,
                                                   State& st, KRing& kr, StartNext&& start_next) {
-        const int lane = threadIdx.x;
+        const int lane = lane_id();
         const int hh = lane & 1;                 // token half (QK and PV)
         const int jq = q_block(w.lnb);           // QK: block of the window
         const int ds = q_slice(w.lnb);           // QK: head_dim slice
@@ -644,13 +647,13 @@ struct Attn {
 
     // lanes 2r and 2r+1 hold identical sums for rows 32i + r: they split the heads
     __device__ __forceinline__ static bool writes_head(int g) {
-        const int hh = threadIdx.x & 1;
+        const int hh = lane_id() & 1;
         return G == 1 ? hh == 0 : (g & 1) == hh;
     }
 
     // final output rows (s, h*G + g)
     __device__ __forceinline__ static void store_out(const DecodeArgs& a, int s, int h, const State& st) {
-        const int jl = threadIdx.x >> 1;
+        const int jl = lane_id() >> 1;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             if (!writes_head(g)) continue;
@@ -669,7 +672,7 @@ struct Attn {
     __device__ __forceinline__ static void store_partial(float* o_base, int64_t o_head_stride,
                                                          float* ml_base, int64_t ml_head_stride,
                                                          const State& st) {
-        const int jl = threadIdx.x >> 1;
+        const int jl = lane_id() >> 1;
         auto put = [](float* p, float v) {
             if constexpr (AGENT)
                 __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
@@ -807,11 +810,11 @@ __device__ __forceinline__ void publish_partials() {
 // for the next call.
 __device__ __forceinline__ bool arrive_last(uint32_t* arrivals, int owner, int pieces) {
     uint32_t old = 0;
-    if (threadIdx.x == 0)
+    if (lane_id() == 0)
         old = __hip_atomic_fetch_add(arrivals + owner, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     const bool last = old == static_cast<uint32_t>(pieces - 1);
-    if (last && threadIdx.x == 0)
+    if (last && lane_id() == 0)
         __hip_atomic_store(arrivals + owner, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return last;
 }
@@ -825,7 +828,7 @@ __device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int s, int 
     using qtag = typename QT<QKIND>::tag;
     constexpr int PER_LANE = D / 64;
     constexpr int MC = G * (2 + PER_LANE) <= 16 ? 8 : 4;
-    const int lane = threadIdx.x;
+    const int lane = lane_id();
     float M[G], L[G], acc[G][PER_LANE];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -877,14 +880,18 @@ __device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int s, int 
     }
 }
 
-template <int QKIND, int KVKIND, int D, int G>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void decode_stream_kernel(DecodeArgs a) {
+template <int QKIND, int KVKIND, int D, int G, int WPB>
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(2))) void decode_stream_kernel(DecodeArgs a) {
     using A = Attn<QKIND, KVKIND, D, G>;
     using qtag = typename QT<QKIND>::tag;
-    __shared__ __align__(16) typename A::QP qp;
-    __shared__ __align__(16) typename A::PL pl;
-    const int w = blockIdx.x, nw = a.num_waves;
-    const int lane = threadIdx.x;
+    __shared__ __align__(16) typename A::QP qp_all[WPB];
+    __shared__ __align__(16) typename A::PL pl_all[WPB];
+    const int wid = WPB == 1 ? 0 : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int w = static_cast<int>(blockIdx.x) * WPB + wid, nw = a.num_waves;
+    if (w >= nw) return;   // waves past the last share (the grid is rounded up to whole workgroups)
+    auto& qp = qp_all[wid];
+    auto& pl = pl_all[wid];
+    const int lane = lane_id();
     const int hkv = a.num_kv_heads;
 
     // Context lengths of sequences 0..63, one per lane: this one load serves
@@ -1013,6 +1020,13 @@ namespace {
 // a stream-mode wave gets at least this many cache blocks of work on average
 constexpr int64_t MIN_STREAM_BLOCKS_PER_WAVE = 32;
 
+// waves per stream-mode workgroup (each wave still walks its own share); 4 and
+// 8 measured within noise of 1 at the benchmark shapes
+#ifndef RLLM_STREAM_WPB
+#define RLLM_STREAM_WPB 1
+#endif
+constexpr int STREAM_WPB = RLLM_STREAM_WPB;
+
 enum class Mode { Stream, Partitioned };
 
 struct Plan {
@@ -1028,7 +1042,7 @@ struct Plan {
 std::mutex g_occ_mutex;
 std::map<std::pair<int, const void*>, int> g_occ;
 
-int resident_waves(const void* kernel) {
+int resident_waves(const void* kernel, int wpb) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     std::lock_guard<std::mutex> lk(g_occ_mutex);
@@ -1036,8 +1050,8 @@ int resident_waves(const void* kernel) {
     if (it != g_occ.end()) return it->second;
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, 0) != hipSuccess) return 0;
-    const int n = cus * per_cu;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64 * wpb, 0) != hipSuccess) return 0;
+    const int n = cus * per_cu * wpb;
     g_occ[{dev, kernel}] = n;
     return n;
 }
@@ -1129,7 +1143,7 @@ struct Kernels {
 template <int QKIND, int KVKIND, int D, int G>
 Kernels kernels_of() {
     return {reinterpret_cast<const void*>(&decode_kernel<QKIND, KVKIND, D, G>),
-            reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G>),
+            reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB>),
             reinterpret_cast<const void*>(&decode_reduce_kernel<QKIND, D>)};
 }
 
@@ -1168,9 +1182,9 @@ bool pick_kernels(int32_t q_dtype, int32_t kv_dtype, int64_t D, int64_t G, Kerne
     }
 }
 
-int32_t launch(const void* kernel, dim3 grid, const DecodeArgs& a, hipStream_t st) {
+int32_t launch(const void* kernel, dim3 grid, const DecodeArgs& a, hipStream_t st, int wpb = 1) {
     void* args[] = {const_cast<DecodeArgs*>(&a)};
-    RLLM_TRY(hipLaunchKernel(kernel, grid, dim3(64), args, 0, st));
+    RLLM_TRY(hipLaunchKernel(kernel, grid, dim3(64 * wpb), args, 0, st));
     return 0;
 }
 
@@ -1198,7 +1212,7 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
 
     Plan plan;
     if (partition_size == 0) {
-        const int res = resident_waves(kern.stream);
+        const int res = resident_waves(kern.stream, STREAM_WPB);
         if (res <= 0) return (int32_t)hipErrorInvalidDeviceFunction;
         plan.mode = Mode::Stream;
         const int max_waves = max_resident_waves();
@@ -1250,7 +1264,8 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
     hipStream_t st = as_stream(stream);
     int32_t rc;
     if (plan.mode == Mode::Stream) {
-        rc = launch(kern.stream, dim3(static_cast<unsigned>(plan.num_waves)), a, st);
+        rc = launch(kern.stream, dim3(static_cast<unsigned>((plan.num_waves + STREAM_WPB - 1) / STREAM_WPB)), a, st,
+                    STREAM_WPB);
     } else {
         rc = launch(kern.part, dim3(static_cast<unsigned>(num_seqs * hkv * plan.max_parts)), a, st);
         if (!rc && plan.max_parts > 1)
