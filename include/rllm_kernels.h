@@ -286,6 +286,26 @@ int32_t rllm_cache_write_fp8_scaled(uint8_t *key_cache, uint8_t *value_cache,
                                     int64_t num_blocks, int32_t input_dtype, float k_scale,
                                     float v_scale, int32_t is_e5m2, uintptr_t stream);
 
+/* New: FP8 write of x / scale with a choice of rounding.  cache_dtype is
+ * RLLM_DTYPE_FP8_E4M3 or RLLM_DTYPE_FP8_E5M2; rounding is
+ *   RLLM_FP8_ROUND_TOWARD_ZERO    the reference contract (cache_ops.cu:13-46,
+ *                                 75-103), identical to rllm_cache_write_fp8_scaled;
+ *   RLLM_FP8_ROUND_NEAREST_EVEN   OCP rounding to nearest, ties to even, with
+ *                                 FP8 subnormals (gradual underflow); values
+ *                                 at or above the largest finite value and
+ *                                 infinities saturate to it, NaN -> 0x7F.
+ * Round toward zero shrinks every stored magnitude (by about 4% on average
+ * for E4M3); nearest-even removes that bias.  Both decode with the same
+ * attention kernels.  Other arguments as rllm_cache_write_fp8_scaled. */
+#define RLLM_FP8_ROUND_TOWARD_ZERO 0
+#define RLLM_FP8_ROUND_NEAREST_EVEN 1
+int32_t rllm_cache_write_fp8_ex(uint8_t *key_cache, uint8_t *value_cache, const uint16_t *new_key,
+                                const uint16_t *new_value, const int64_t *slot_mapping,
+                                int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim,
+                                int64_t block_size, int64_t num_blocks, int32_t input_dtype,
+                                float k_scale, float v_scale, int32_t cache_dtype,
+                                int32_t rounding, uintptr_t stream);
+
 /* New (additive): rotary position embedding fused with the cache write.  It
  * replaces the model-side sequence RotaryEmbedding::apply (rope.rs:34-43,
  * 57-82: q and k rotated by halves, x*cos + rotate_half(x)*sin in the

@@ -58,6 +58,14 @@ def lib() -> ctypes.CDLL:
     for name in ("orc_fp8_e4m3_exhaustive", "orc_fp8_e5m2_exhaustive"):
         getattr(L, name).argtypes = [c.c_int, c.POINTER(c.c_uint32)]
         getattr(L, name).restype = i64
+    for name in ("orc_fp8_e4m3_encode_rne", "orc_fp8_e5m2_encode_rne"):
+        getattr(L, name).argtypes = [c.c_float]
+        getattr(L, name).restype = c.c_uint8
+    L.orc_encode_fp8_rne_array.argtypes = [P, c.c_int, i64, P]
+    L.orc_fp8_rne_exhaustive.argtypes = [c.c_int, c.c_int, c.POINTER(c.c_uint32)]
+    L.orc_fp8_rne_exhaustive.restype = i64
+    L.orc_cache_write_rounded.argtypes = [P, P, P, P, P, i64, i64, i64, i64, i64, c.c_int, c.c_int,
+                                          c.c_float, c.c_float, c.c_int]
     L.orc_slot_mapping.argtypes = [P, i64, P, i64, i64, P]
     L.orc_cache_write.argtypes = [P, P, P, P, P, i64, i64, i64, i64, i64, c.c_int, c.c_int,
                                   c.c_float, c.c_float]
@@ -107,6 +115,22 @@ def encode(x: np.ndarray, kind: int) -> np.ndarray:
     return out
 
 
+def encode_fp8_rne(x: np.ndarray, kind: int) -> np.ndarray:
+    """float32 -> FP8 bytes rounded to nearest even (the library's opt-in mode)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib().orc_encode_fp8_rne_array(_p(x), kind, x.size, _p(out))
+    return out
+
+
+def fp8_rne_exhaustive(e5m2: bool = False, nthreads: int = 8) -> tuple[int, int]:
+    """(violations, first violating pattern) of the nearest-even encoder over
+    all 2^32 float32 patterns."""
+    bad_pat = ctypes.c_uint32(0)
+    bad = lib().orc_fp8_rne_exhaustive(1 if e5m2 else 0, nthreads, ctypes.byref(bad_pat))
+    return int(bad), int(bad_pat.value)
+
+
 def fp8_exhaustive(e5m2: bool = False, nthreads: int = 8) -> tuple[int, int]:
     bad_pat = ctypes.c_uint32(0)
     fn = lib().orc_fp8_e5m2_exhaustive if e5m2 else lib().orc_fp8_e4m3_exhaustive
@@ -125,14 +149,17 @@ def slot_mapping(positions, block_table, block_size: int) -> np.ndarray:
 
 
 def cache_write(key_cache, value_cache, new_key, new_value, slot_mapping, block_size: int,
-                in_kind: int, cache_kind: int, k_scale: float = 1.0, v_scale: float = 1.0):
-    """In place on numpy caches of shape [nb, Hkv, D, bs]."""
+                in_kind: int, cache_kind: int, k_scale: float = 1.0, v_scale: float = 1.0,
+                round_nearest: bool = False):
+    """In place on numpy caches of shape [nb, Hkv, D, bs]; ``round_nearest``
+    selects the nearest-even FP8 encoders instead of the reference's
+    round-toward-zero."""
     nb, hkv, d, bs = key_cache.shape
     assert bs == block_size
     sm = np.ascontiguousarray(slot_mapping, dtype=np.int64)
-    lib().orc_cache_write(_p(key_cache), _p(value_cache), _p(np.ascontiguousarray(new_key)),
-                          _p(np.ascontiguousarray(new_value)), _p(sm), sm.size, hkv, d, bs, nb,
-                          in_kind, cache_kind, k_scale, v_scale)
+    lib().orc_cache_write_rounded(_p(key_cache), _p(value_cache), _p(np.ascontiguousarray(new_key)),
+                                  _p(np.ascontiguousarray(new_value)), _p(sm), sm.size, hkv, d, bs, nb,
+                                  in_kind, cache_kind, k_scale, v_scale, 1 if round_nearest else 0)
 
 
 def rope_interleaved(x, positions, theta: float):

@@ -135,6 +135,39 @@ float orc_fp8_e5m2_decode(uint8_t b) {
     return sign ? -v : v;
 }
 
+/* Round to nearest, ties to even (the library's opt-in FP8 mode, OCP
+ * E4M3FN / E5M2 with subnormals, saturating).  Written in double arithmetic
+ * on the value, independently of the library's bit manipulation: the
+ * quantum at |x| is 2^(max(floor(log2|x|), emin) - mbits), and rint()
+ * rounds |x| / quantum to nearest even (the default rounding mode). */
+static uint8_t fp8_rne(float x, int mbits, int emin, int bias, double maxf) {
+    if (isnan(x)) return 0x7F;
+    uint8_t sign = signbit(x) ? 0x80 : 0x00;
+    double a = fabs((double)x);
+    if (a >= maxf) a = maxf;                               /* saturate (incl. inf) */
+    if (a == 0.0) return sign;
+    int e = ilogb(a);
+    if (e < emin) e = emin;
+    double quantum = ldexp(1.0, e - mbits);
+    double k = rint(a / quantum);                          /* exact scaling, RNE */
+    double v = k * quantum;
+    if (v == 0.0) return sign;
+    int ve = ilogb(v);
+    if (ve < emin) return (uint8_t)(sign | (uint8_t)k);    /* subnormal: k quanta of 2^(emin - mbits) */
+    uint32_t field = (uint32_t)(ve + bias);
+    uint32_t mant = (uint32_t)(ldexp(v, -ve) * (1 << mbits)) - (1u << mbits);
+    return (uint8_t)(sign | (field << mbits) | mant);
+}
+
+uint8_t orc_fp8_e4m3_encode_rne(float x) { return fp8_rne(x, 3, -6, 7, 448.0); }
+
+uint8_t orc_fp8_e5m2_encode_rne(float x) { return fp8_rne(x, 2, -14, 15, 57344.0); }
+
+void orc_encode_fp8_rne_array(const float *src, int kind, int64_t n, uint8_t *dst) {
+    for (int64_t i = 0; i < n; i++)
+        dst[i] = kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode_rne(src[i]) : orc_fp8_e5m2_encode_rne(src[i]);
+}
+
 static inline float decode_elem(const void *base, int kind, int64_t i) {
     switch (kind) {
     case ORC_F16: return orc_f16_to_f32(((const uint16_t *)base)[i]);
@@ -237,6 +270,75 @@ static int64_t run_exhaustive(int e5m2, int nthreads, uint32_t *first_bad) {
     return bad;
 }
 
+/* Nearest-even characterisation, written against the decoder only: the
+ * byte decodes to a finite value no farther from x (clamped to the largest
+ * finite value) than either neighbouring code, and on a tie its code is even.
+ * NaN -> 0x7F; the sign bit follows x. */
+static int rne_ok(uint32_t u, int e5m2) {
+    float x = u2f(u);
+    uint8_t b = e5m2 ? orc_fp8_e5m2_encode_rne(x) : orc_fp8_e4m3_encode_rne(x);
+    if (isnan(x)) return b == 0x7F;
+    if ((b & 0x80) != ((u >> 24) & 0x80)) return 0;
+    uint8_t mag = b & 0x7F, top = e5m2 ? 0x7B : 0x7E;
+    if (mag > top) return 0;
+    double a = fabs((double)x), lim = e5m2 ? 57344.0 : 448.0;
+    if (a > lim) a = lim;
+    double v = e5m2 ? fabs((double)orc_fp8_e5m2_decode(mag)) : fabs((double)orc_fp8_e4m3_decode(mag));
+    double err = fabs(v - a);
+    for (int d = -1; d <= 1; d += 2) {
+        int nb = (int)mag + d;
+        if (nb < 0 || nb > top) continue;
+        double w = e5m2 ? fabs((double)orc_fp8_e5m2_decode((uint8_t)nb))
+                        : fabs((double)orc_fp8_e4m3_decode((uint8_t)nb));
+        double e2 = fabs(w - a);
+        if (e2 < err) return 0;
+        if (e2 == err && (mag & 1u)) return 0;
+    }
+    return 1;
+}
+
+typedef struct {
+    uint64_t lo, hi;
+    int e5m2;
+    int64_t bad;
+    uint32_t first_bad;
+} rne_job;
+
+static void *rne_worker(void *p) {
+    rne_job *j = (rne_job *)p;
+    for (uint64_t v = j->lo; v < j->hi; v++) {
+        if (!rne_ok((uint32_t)v, j->e5m2)) {
+            if (j->bad == 0) j->first_bad = (uint32_t)v;
+            j->bad++;
+        }
+    }
+    return NULL;
+}
+
+int64_t orc_fp8_rne_exhaustive(int e5m2, int nthreads, uint32_t *first_bad) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    rne_job jobs[256];
+    uint64_t total = 1ull << 32, step = (total + nthreads - 1) / nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        jobs[t].lo = step * t;
+        jobs[t].hi = step * (t + 1) < total ? step * (t + 1) : total;
+        jobs[t].e5m2 = e5m2;
+        jobs[t].bad = 0;
+        jobs[t].first_bad = 0;
+        pthread_create(&th[t], NULL, rne_worker, &jobs[t]);
+    }
+    int64_t bad = 0;
+    int have = 0;
+    for (int t = 0; t < nthreads; t++) {
+        pthread_join(th[t], NULL);
+        if (jobs[t].bad && !have) { have = 1; if (first_bad) *first_bad = jobs[t].first_bad; }
+        bad += jobs[t].bad;
+    }
+    return bad;
+}
+
 int64_t orc_fp8_e4m3_exhaustive(int nthreads, uint32_t *first_bad) {
     return run_exhaustive(0, nthreads, first_bad);
 }
@@ -268,6 +370,16 @@ void orc_cache_write(void *key_cache, void *value_cache, const void *new_key,
                      int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
                      int64_t num_blocks, int in_kind, int cache_kind, float k_scale,
                      float v_scale) {
+    orc_cache_write_rounded(key_cache, value_cache, new_key, new_value, slot_mapping, num_tokens,
+                            num_kv_heads, head_dim, block_size, num_blocks, in_kind, cache_kind,
+                            k_scale, v_scale, 0);
+}
+
+void orc_cache_write_rounded(void *key_cache, void *value_cache, const void *new_key,
+                             const void *new_value, const int64_t *slot_mapping, int64_t num_tokens,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                             int64_t num_blocks, int in_kind, int cache_kind, float k_scale,
+                             float v_scale, int round_nearest) {
     for (int64_t t = 0; t < num_tokens; t++) {
         int64_t slot = slot_mapping[t];
         if (slot < 0) continue;
@@ -283,10 +395,14 @@ void orc_cache_write(void *key_cache, void *value_cache, const void *new_key,
                 } else {
                     float kx = decode_elem(new_key, in_kind, src) / k_scale;
                     float vx = decode_elem(new_value, in_kind, src) / v_scale;
-                    uint8_t kb = cache_kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode(kx)
-                                                            : orc_fp8_e5m2_encode(kx);
-                    uint8_t vb = cache_kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode(vx)
-                                                            : orc_fp8_e5m2_encode(vx);
+                    uint8_t kb = round_nearest ? (cache_kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode_rne(kx)
+                                                                             : orc_fp8_e5m2_encode_rne(kx))
+                                               : (cache_kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode(kx)
+                                                                             : orc_fp8_e5m2_encode(kx));
+                    uint8_t vb = round_nearest ? (cache_kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode_rne(vx)
+                                                                             : orc_fp8_e5m2_encode_rne(vx))
+                                               : (cache_kind == ORC_FP8_E4M3 ? orc_fp8_e4m3_encode(vx)
+                                                                             : orc_fp8_e5m2_encode(vx));
                     ((uint8_t *)key_cache)[dst] = kb;
                     ((uint8_t *)value_cache)[dst] = vb;
                 }

@@ -77,6 +77,13 @@ void orc_encode_array(const float *src, int kind, int64_t n, void *dst);
 int64_t orc_fp8_e4m3_exhaustive(int nthreads, uint32_t *first_bad);
 /* Same for the E5M2 encoder. */
 int64_t orc_fp8_e5m2_exhaustive(int nthreads, uint32_t *first_bad);
+/* Round to nearest even (the library's opt-in FP8 mode): OCP E4M3FN / E5M2
+ * with subnormals, saturating at the largest finite value, NaN -> 0x7F. */
+uint8_t orc_fp8_e4m3_encode_rne(float x);
+uint8_t orc_fp8_e5m2_encode_rne(float x);
+void orc_encode_fp8_rne_array(const float *src, int kind, int64_t n, uint8_t *dst);
+/* All 2^32 float32 patterns against the nearest-even characterisation. */
+int64_t orc_fp8_rne_exhaustive(int e5m2, int nthreads, uint32_t *first_bad);
 
 /* ---- slot mapping (model_runner.rs:806-826) ------------------------- */
 void orc_slot_mapping(const uint32_t *positions, int64_t n, const uint32_t *block_table,
@@ -91,6 +98,12 @@ void orc_cache_write(void *key_cache, void *value_cache, const void *new_key,
                      int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
                      int64_t num_blocks, int in_kind, int cache_kind, float k_scale,
                      float v_scale);
+/* As orc_cache_write; round_nearest selects the nearest-even FP8 encoders. */
+void orc_cache_write_rounded(void *key_cache, void *value_cache, const void *new_key,
+                             const void *new_value, const int64_t *slot_mapping, int64_t num_tokens,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                             int64_t num_blocks, int in_kind, int cache_kind, float k_scale,
+                             float v_scale, int round_nearest);
 
 /* ---- RMSNorm and SiLU-mul (layers.rs:128-140, 214-220) --------------------
  * The model's ops in the activation dtype (kinds ORC_F16 / ORC_BF16), with

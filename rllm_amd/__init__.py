@@ -5,13 +5,13 @@ The product is ``librllm_kernels.so`` (HIP kernels + C ABI, declared in
 host-side mirror of the reference's Rust wrappers (``attention``,
 ``cache_ops``), and a torch-tensor front end (``ops``).
 """
-from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_FP8_E4M3, DTYPE_FP8_E5M2, HEADER_PATH,
-                   LIB_PATH, KernelError, NotAvailable, lib)
+from ._lib import (DTYPE_BF16, DTYPE_F16, DTYPE_FP8_E4M3, DTYPE_FP8_E5M2, FP8_ROUND_NEAREST_EVEN,
+                   FP8_ROUND_TOWARD_ZERO, HEADER_PATH, LIB_PATH, KernelError, NotAvailable, lib)
 from .attention import AttentionMetadata, AttentionParams
 from .cache_ops import GpuKVCache, compute_slot_mappings
 
 __all__ = [
     "AttentionMetadata", "AttentionParams", "GpuKVCache", "KernelError", "NotAvailable",
     "compute_slot_mappings", "lib", "LIB_PATH", "HEADER_PATH", "DTYPE_F16", "DTYPE_BF16",
-    "DTYPE_FP8_E4M3", "DTYPE_FP8_E5M2",
+    "DTYPE_FP8_E4M3", "DTYPE_FP8_E5M2", "FP8_ROUND_TOWARD_ZERO", "FP8_ROUND_NEAREST_EVEN",
 ]

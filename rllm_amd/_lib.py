@@ -16,6 +16,8 @@ LIB_PATH = os.path.join(PKG_DIR, "librllm_kernels.so")
 HEADER_PATH = os.path.join(os.path.dirname(PKG_DIR), "include", "rllm_kernels.h")
 
 DTYPE_F16, DTYPE_BF16, DTYPE_FP8_E4M3, DTYPE_FP8_E5M2 = 0, 1, 2, 3
+# FP8 rounding of the cache writes (RLLM_FP8_ROUND_* in include/rllm_kernels.h)
+FP8_ROUND_TOWARD_ZERO, FP8_ROUND_NEAREST_EVEN = 0, 1
 
 
 class KernelError(RuntimeError):
@@ -63,6 +65,7 @@ SIGNATURES = {
     "rllm_cache_write_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _U],
     "rllm_cache_write_fp8_sync": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32],
     "rllm_cache_write_fp8_scaled": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _F, _F, _I32, _U],
+    "rllm_cache_write_fp8_ex": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _F, _F, _I32, _I32, _U],
     "rllm_rope_cache_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                               _I64, _I64, _I32, _I32, _F, _F, _U],
     "rllm_rope_tables": [_P, _P, _I64, _I64, _F],

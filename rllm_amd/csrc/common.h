@@ -107,6 +107,56 @@ __host__ __device__ __forceinline__ uint8_t fp8_e5m2_encode(float x) {
 }
 
 // ---------------------------------------------------------------------------
+// FP8 encoders rounding to nearest, ties to even (the opt-in alternative to
+// the reference contract): OCP E4M3FN / E5M2 with gradual underflow to the
+// FP8 subnormals; magnitudes at or above the largest finite value and
+// infinities saturate to it; NaN -> 0x7F.  Integer-only bit arithmetic.
+// ---------------------------------------------------------------------------
+// Rounds the magnitude a (f32 bits, finite, below the format's largest
+// finite value) to a format with MB mantissa bits and exponent bias EB.
+template <int MB, int EB>
+__host__ __device__ __forceinline__ uint32_t fp8_round_nearest(uint32_t a) {
+    const int e = static_cast<int>(a >> 23);          // f32 biased exponent
+    constexpr int E_MIN = 127 - EB + 1;               // f32 exponent of the smallest normal
+    if (e >= E_MIN) {                                  // normal: keep MB mantissa bits
+        constexpr int SH = 23 - MB;
+        uint32_t q = (static_cast<uint32_t>(e - (127 - EB)) << MB) | ((a & 0x7fffffu) >> SH);
+        const uint32_t rem = a & ((1u << SH) - 1u), half = 1u << (SH - 1);
+        if (rem > half || (rem == half && (q & 1u))) ++q;   // a carry moves into the exponent
+        return q;
+    }
+    if (e == 0) return 0;                              // f32 subnormal: far below half the FP8 quantum
+    // subnormal: k = |x| / 2^(1 - EB - MB), rounded; k = 2^MB is the smallest normal
+    const uint32_t sig = (a & 0x7fffffu) | 0x800000u;  // |x| = sig * 2^(e - 150)
+    const int sh = (1 - EB - MB) + 150 - e;            // k = sig >> sh
+    if (sh >= 25) return 0;                            // below half of the quantum (sig < 2^24)
+    uint32_t k = sig >> sh;
+    const uint32_t rem = sig & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (k & 1u))) ++k;
+    return k;
+}
+
+__host__ __device__ __forceinline__ uint8_t fp8_e4m3_encode_rne(float x) {
+    uint32_t u;
+    __builtin_memcpy(&u, &x, 4);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0x7F;                  // NaN
+    if (a >= 0x43E00000u) return static_cast<uint8_t>(sign | 0x7Eu);   // >= 448 (incl. inf)
+    return static_cast<uint8_t>(sign | fp8_round_nearest<3, 7>(a));
+}
+
+__host__ __device__ __forceinline__ uint8_t fp8_e5m2_encode_rne(float x) {
+    uint32_t u;
+    __builtin_memcpy(&u, &x, 4);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0x7F;
+    if (a >= 0x47600000u) return static_cast<uint8_t>(sign | 0x7Bu);   // >= 57344 (incl. inf)
+    return static_cast<uint8_t>(sign | fp8_round_nearest<2, 15>(a));
+}
+
+// ---------------------------------------------------------------------------
 // wave64 helpers
 // ---------------------------------------------------------------------------
 // DPP quad permutations: xor 1 = [1,0,3,2], xor 2 = [2,3,0,1]

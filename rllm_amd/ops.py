@@ -11,7 +11,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import DTYPE_BF16, DTYPE_F16, DTYPE_FP8_E4M3, DTYPE_FP8_E5M2, call
+from ._lib import DTYPE_BF16, DTYPE_F16, DTYPE_FP8_E4M3, DTYPE_FP8_E5M2, FP8_ROUND_TOWARD_ZERO, call
 
 _TORCH_16 = {torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
@@ -138,8 +138,11 @@ def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
 def reshape_and_cache(new_key: torch.Tensor, new_value: torch.Tensor, k_cache: torch.Tensor,
                       v_cache: torch.Tensor, slot_mapping: torch.Tensor, *,
                       kv_dtype: Optional[int] = None, k_scale: float = 1.0, v_scale: float = 1.0,
+                      fp8_rounding: int = FP8_ROUND_TOWARD_ZERO,
                       stream: Optional[torch.cuda.Stream] = None) -> None:
-    """Slot-mapped cache write through rllm_cache_write_{bf16,f16,fp8_scaled}."""
+    """Slot-mapped cache write through rllm_cache_write_{bf16,f16,fp8_ex}.
+    ``fp8_rounding``: FP8_ROUND_TOWARD_ZERO (the reference contract) or
+    FP8_ROUND_NEAREST_EVEN."""
     if new_key.shape != new_value.shape or new_key.dim() != 3:
         raise ValueError("new_key/new_value must be [num_tokens, Hkv, D]")
     n, hkv, d = new_key.shape
@@ -163,9 +166,9 @@ def reshape_and_cache(new_key: torch.Tensor, new_value: torch.Tensor, k_cache: t
         call(name, _ptr(k_cache), _ptr(v_cache), _ptr(new_key), _ptr(new_value),
              _ptr(slot_mapping), n, hkv, d, bs, nb, st)
     else:
-        call("rllm_cache_write_fp8_scaled", _ptr(k_cache), _ptr(v_cache), _ptr(new_key),
+        call("rllm_cache_write_fp8_ex", _ptr(k_cache), _ptr(v_cache), _ptr(new_key),
              _ptr(new_value), _ptr(slot_mapping), n, hkv, d, bs, nb, ind, k_scale, v_scale,
-             1 if kv == DTYPE_FP8_E5M2 else 0, st)
+             kv, fp8_rounding, st)
 
 
 def rope_cache_tables(max_position: int, head_dim: int, theta: float = 10000.0,

@@ -163,3 +163,55 @@ def test_cache_write_invalid_arguments(dev):
         C.cache_write_fp8_scaled(ptr(buf), ptr(buf), ptr(buf), ptr(buf), ptr(buf), 1, 1, 1, 16, 1,
                                  rllm_amd.DTYPE_BF16, 0.0, 1.0, 0)  # zero scale
     C.cache_write_f16(0, 0, 0, 0, 0, 0, 8, 128, 16, 10)           # empty work -> 0
+
+
+@pytest.mark.parametrize("fp8", [O.FP8_E4M3, O.FP8_E5M2])
+@pytest.mark.parametrize("dt,kind", [(torch.bfloat16, O.BF16), (torch.float16, O.F16)])
+@pytest.mark.parametrize("scales", [(1.0, 1.0), (2.0 ** -7, 2.0 ** 9), (3.7 / 448.0, 0.0117)])
+def test_cache_write_fp8_nearest_even_every_input_pattern(dev, fp8, dt, kind, scales):
+    """rllm_cache_write_fp8_ex with RLLM_FP8_ROUND_NEAREST_EVEN: every 16-bit
+    input pattern (NaN, infinities, subnormals, ties after scaling), divided
+    by power-of-two scales (reciprocal path) and other scales (division path),
+    bit-exact against the oracle's nearest-even encoder."""
+    hkv, d, bs = 8, 128, 16
+    bits = np.arange(65536, dtype=np.uint16).reshape(-1, hkv, d)      # 64 tokens
+    n = bits.shape[0]
+    nb = n // bs + 2
+    rng = np.random.default_rng(fp8 * 7 + kind)
+    sl = rng.permutation(nb * bs)[:n].astype(np.int64)
+    kc = rng.integers(0, 256, size=(nb, hkv, d, bs), dtype=np.uint8)
+    vc = rng.integers(0, 256, size=(nb, hkv, d, bs), dtype=np.uint8)
+    nv = bits[::-1].copy()
+    gk, gv = t8(kc, dev), t8(vc, dev)
+    log_case(f"cache_write fp8 nearest-even fp8={fp8} in={kind} scales={scales}")
+    ops.reshape_and_cache(t16(bits, dt, dev), t16(nv, dt, dev), gk, gv, ti(sl, torch.int64, dev),
+                          kv_dtype=rllm_amd.DTYPE_FP8_E4M3 if fp8 == O.FP8_E4M3 else rllm_amd.DTYPE_FP8_E5M2,
+                          k_scale=scales[0], v_scale=scales[1],
+                          fp8_rounding=rllm_amd.FP8_ROUND_NEAREST_EVEN)
+    torch.cuda.synchronize()
+    ek, ev = kc.copy(), vc.copy()
+    O.cache_write(ek, ev, bits, nv, sl, bs, kind, fp8, scales[0], scales[1], round_nearest=True)
+    assert np.array_equal(gk.cpu().numpy(), ek) and np.array_equal(gv.cpu().numpy(), ev)
+
+
+def test_cache_write_fp8_ex_round_toward_zero_is_the_scaled_write(dev):
+    rng = np.random.default_rng(21)
+    nb, hkv, d, bs, n = 12, 4, 64, 16, 100
+    nk = O.encode(rng.standard_normal((n, hkv, d)).astype(np.float32) * 50, O.BF16)
+    nv = O.encode(rng.standard_normal((n, hkv, d)).astype(np.float32) * 50, O.BF16)
+    sl = _slots(rng, nb, bs, n)
+    kc = np.zeros((nb, hkv, d, bs), np.uint8)
+    gk, gv = t8(kc, dev), t8(kc, dev)
+    log_case("rllm_cache_write_fp8_ex toward zero")
+    ops.reshape_and_cache(t16(nk, torch.bfloat16, dev), t16(nv, torch.bfloat16, dev), gk, gv,
+                          ti(sl, torch.int64, dev), kv_dtype=rllm_amd.DTYPE_FP8_E5M2, k_scale=0.3,
+                          v_scale=0.05, fp8_rounding=rllm_amd.FP8_ROUND_TOWARD_ZERO)
+    torch.cuda.synchronize()
+    ek, ev = kc.copy(), kc.copy()
+    O.cache_write(ek, ev, nk, nv, sl, bs, O.BF16, O.FP8_E5M2, 0.3, 0.05)
+    assert np.array_equal(gk.cpu().numpy(), ek) and np.array_equal(gv.cpu().numpy(), ev)
+    P = gk.data_ptr()
+    L = rllm_amd.lib()
+    # bad rounding mode or a 16-bit cache dtype: rejected before any launch
+    assert L.rllm_cache_write_fp8_ex(P, P, P, P, P, 4, 8, 128, 16, 10, 1, 1.0, 1.0, 2, 2, 0) == 1
+    assert L.rllm_cache_write_fp8_ex(P, P, P, P, P, 4, 8, 128, 16, 10, 1, 1.0, 1.0, 1, 1, 0) == 1

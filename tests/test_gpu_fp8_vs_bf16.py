@@ -1,0 +1,59 @@
+"""FP8 KV against the bf16 KV run on the same data (config 3's per-sequence
+shape: 32/8 heads, head_dim 128, context 2048): the bf16 cache is quantised
+by the library's own cache write with per-tensor scales amax / max_finite, and
+both caches are attended by the library's decode kernels.  The elementwise
+bound is the FP8 tolerance (5e-2 + 5e-2|b|); the relative L2 error is
+reported and bounded per rounding mode.  Round toward zero (the reference
+contract, cache_ops.cu:13-46, 75-103) shrinks every stored magnitude, which
+shows as a bias of the output (E4M3 ~9-10% relative L2 on N(0,1) data);
+nearest-even (RLLM_FP8_ROUND_NEAREST_EVEN) meets the 5e-2 E4M3 target.
+The oracle's float64 attention over the same FP8 bytes gives the same
+figures (within 1e-3)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import rllm_amd
+from gpu_util import f32, log_case, t16, ti
+from helpers import TOL_FP8, assert_close, random_case
+from rllm_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+# (kv dtype, rounding) -> bound on the relative L2 error against the bf16 run
+CASES = [(rllm_amd.DTYPE_FP8_E4M3, rllm_amd.FP8_ROUND_NEAREST_EVEN, 5e-2),
+         (rllm_amd.DTYPE_FP8_E4M3, rllm_amd.FP8_ROUND_TOWARD_ZERO, 0.12),
+         (rllm_amd.DTYPE_FP8_E5M2, rllm_amd.FP8_ROUND_NEAREST_EVEN, 0.10),
+         (rllm_amd.DTYPE_FP8_E5M2, rllm_amd.FP8_ROUND_TOWARD_ZERO, 0.22)]
+
+
+@pytest.mark.parametrize("kv,rounding,bound", CASES, ids=["e4m3-rne", "e4m3-rtz", "e5m2-rne", "e5m2-rtz"])
+def test_fp8_kv_against_bf16_kv(dev, kv, rounding, bound):
+    rng = np.random.default_rng(0x524C4C4D ^ 3)
+    B, hq, hkv, D, bs = 32, 32, 8, 128, 16
+    q, k, v, bt, sl = random_case(rng, B, hq, hkv, D, (2048, 2048))
+    qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
+    gq, gk, gv = t16(qb, torch.bfloat16, dev), t16(kb, torch.bfloat16, dev), t16(vb, torch.bfloat16, dev)
+    gbt, gsl = ti(bt, torch.int32, dev), ti(sl, torch.int32, dev)
+    scale = 1 / np.sqrt(D)
+    log_case(f"fp8 vs bf16 kv={kv} rounding={rounding}")
+    ref = f32(ops.paged_decode(gq, gk, gv, gbt, gsl, scale))
+    top = 448.0 if kv == rllm_amd.DTYPE_FP8_E4M3 else 57344.0
+    ks, vs = float(gk.float().abs().max()) / top, float(gv.float().abs().max()) / top
+    nb = gk.shape[0]
+    slots = torch.arange(nb * bs, device=dev, dtype=torch.int64)
+    tok_k = gk.permute(0, 3, 1, 2).reshape(-1, hkv, D).contiguous()
+    tok_v = gv.permute(0, 3, 1, 2).reshape(-1, hkv, D).contiguous()
+    k8 = torch.empty(gk.shape, dtype=torch.uint8, device=dev)
+    v8 = torch.empty_like(k8)
+    ops.reshape_and_cache(tok_k, tok_v, k8, v8, slots, kv_dtype=kv, k_scale=ks, v_scale=vs,
+                          fp8_rounding=rounding)
+    got = f32(ops.paged_decode(gq, k8, v8, gbt, gsl, scale, kv_dtype=kv, k_scale=ks, v_scale=vs))
+    torch.cuda.synchronize()
+    rel_l2 = assert_close(got, ref, TOL_FP8, f"fp8 kv={kv} rounding={rounding} vs bf16 kv")
+    print(f"kv={kv} rounding={rounding}: rel_l2 {rel_l2:.4f} (bound {bound})")
+    assert rel_l2 <= bound
+    if rounding == rllm_amd.FP8_ROUND_NEAREST_EVEN:   # no systematic shrink
+        ratio = float((got * ref).sum() / (ref * ref).sum())
+        assert abs(ratio - 1) < 0.02, ratio
