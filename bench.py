@@ -24,6 +24,7 @@ after the timed region, so a counter run can scale FETCH_SIZE/WRITE_SIZE.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -398,6 +399,9 @@ def main() -> int:
                     help="attention (default): the config's decode or prefill line; rope_cache: the fused "
                          "RoPE + cache write over the config's new tokens; copy_blocks / swap_out / swap_in: "
                          "block-list moves over a 32-layer cache; rmsnorm / silu_mul: at Llama-3-8B widths")
+    ap.add_argument("--tp", type=int, default=1,
+                    help="decode configs: time one GPU's share of a tensor-parallel run "
+                         "(num_q_heads / tp and num_kv_heads / tp at the config's lengths)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
@@ -425,6 +429,13 @@ def main() -> int:
         return bench_fused(args, w, lib, dev)
     if args.config == 5:
         return bench_prefill(args, w, lib, dev)
+    if args.tp > 1:
+        if w.num_kv_heads % args.tp:
+            print(f"--tp {args.tp} does not divide {w.num_kv_heads} kv heads", file=sys.stderr)
+            return 2
+        w = dataclasses.replace(w, name=f"{w.name}_tp{args.tp}_share",
+                                num_q_heads=w.num_q_heads // args.tp,
+                                num_kv_heads=w.num_kv_heads // args.tp)
     fp8 = w.kv_dtype.startswith("fp8")
     qb, kb, vb = workloads.host_tensors(w)
 
@@ -456,6 +467,11 @@ def main() -> int:
     else:
         kc, vc = t16(kb), t16(vb)
         pools = [(kc, vc), (kc.clone(), vc.clone())]
+    # rotate over enough pool copies that a step never finds the previous
+    # steps' KV in the 256 MB MALL (two copies at full size; more for a share)
+    pool_bytes = 2 * pools[0][0].numel() * pools[0][0].element_size()
+    while len(pools) * pool_bytes < 600e6:
+        pools.append((pools[0][0].clone(), pools[0][1].clone()))
     kv_code = rllm_amd.DTYPE_FP8_E4M3 if fp8 else rllm_amd.DTYPE_BF16
     ops.validate_tables(bt, sl, w.num_blocks, w.block_size)
     torch.cuda.synchronize()
@@ -467,7 +483,7 @@ def main() -> int:
     pool_ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in pools]
 
     def step(i):
-        kp, vp = pool_ptrs[i & 1]
+        kp, vp = pool_ptrs[i % len(pool_ptrs)]
         rc = fn(op, qp, kp, vp, btp, slp, w.num_seqs, w.num_q_heads, w.num_kv_heads, w.head_dim,
                 w.block_size, w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, kv_code, k_scale, v_scale,
                 args.partition, None, 0, sh)
@@ -517,7 +533,7 @@ def main() -> int:
                    "head_dim": w.head_dim, "block_size": w.block_size,
                    "sum_context_tokens": int(w.seq_lens.sum()),
                    "max_context": int(w.seq_lens.max()), "partition": args.partition,
-                   "parallelism": "single GPU"},
+                   "parallelism": f"tp{args.tp} share on one GPU" if args.tp > 1 else "single GPU"},
         "seqs_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
