@@ -922,9 +922,13 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(2))) v
         total += __builtin_amdgcn_readlane(wave_scan(nb), 63);
     }
     total *= hkv;
-    const int64_t lo = WorkList::share_begin(total, w, nw);
-    const int64_t hi = WorkList::share_begin(total, w + 1, nw);
-    if (lo >= hi) return;
+    // No share may be empty: a cut row counts its pieces as the shares its
+    // items span, so there are at most as many shares as items (the grid is
+    // sized from the table width, which can exceed the contexts by far).
+    const int nws = static_cast<int>(min(static_cast<int64_t>(nw), total));
+    if (w >= nws) return;
+    const int64_t lo = WorkList::share_begin(total, w, nws);
+    const int64_t hi = WorkList::share_begin(total, w + 1, nws);
 
     // locate the sequence holding item lo
     int s = 0;
@@ -993,8 +997,8 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(2))) v
             // b0 > 0: the wave's first piece (head); else its last (tail)
             const int64_t slot = 2 * static_cast<int64_t>(w) + (p.b0 > 0 ? 0 : 1);
             A::template store_partial<true>(a.part_out + slot * G * D, D, a.part_ml + slot * G * 2, 2, st);
-            const Split sp{p.s, p.h, WorkList::wave_of(total, p.row_item, nw),
-                           WorkList::wave_of(total, p.row_item + p.nb - 1, nw)};
+            const Split sp{p.s, p.h, WorkList::wave_of(total, p.row_item, nws),
+                           WorkList::wave_of(total, p.row_item + p.nb - 1, nws)};
             if (nsplit++ == 0)
                 split0 = sp;
             else

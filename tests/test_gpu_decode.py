@@ -262,6 +262,28 @@ def test_decode_stream_mode_caller_workspace_reused(dev):
         assert_close(f32(out), ref, TOL_BF16, f"stream workspace call {i}")
 
 
+def test_decode_wide_tables_short_rows(dev):
+    """Tables 256 blocks wide holding rows of 1-3 blocks: the grid is sized
+    from the table width, so there are more waves than work items.  Every
+    row cut between shares must still be merged, and the workspace counters
+    must come back zero (two calls on one caller workspace)."""
+    rng = np.random.default_rng(41)
+    B, hq, hkv, D = 64, 32, 8, 128
+    nbytes = A.decode_workspace_size(B, hq, hkv, D, 16, 256, 0)
+    ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    for call in range(2):
+        q, k, v, bt, sl = random_case(rng, B, hq, hkv, D, (1, 48), max_blocks=256)
+        qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
+        ref = oracle_ref(qb, O.BF16, kb, vb, O.BF16, bt, sl, 0.1)
+        log_case(f"wide tables short rows call {call}")
+        out = ops.paged_decode(t16(qb, torch.bfloat16, dev), t16(kb, torch.bfloat16, dev),
+                               t16(vb, torch.bfloat16, dev), ti(bt, torch.int32, dev),
+                               ti(sl, torch.int32, dev), 0.1, partition_size=0, workspace=ws)
+        torch.cuda.synchronize()
+        assert_close(f32(out), ref, TOL_BF16, f"wide tables call {call}")
+    assert int(ws[:16384].view(torch.int32).abs().sum()) == 0   # arrival counters of every unit reset
+
+
 @pytest.mark.parametrize("kind", [O.BF16, O.FP8_E4M3])
 def test_decode_long_rows_split_over_many_waves(dev, kind):
     """Two 40k-token sequences: every (sequence, kv head) row is cut into
