@@ -109,8 +109,27 @@ def bench_prefill(args, w, lib, dev) -> int:
     qb, kb, vb = workloads_host(w)
     t16 = lambda b: torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(dev)
     q = t16(qb)
-    pools = [(t16(kb), t16(vb))]
-    pools.append((pools[0][0].clone(), pools[0][1].clone()))
+    kv_code, k_scale, v_scale = rllm_amd.DTYPE_BF16, 1.0, 1.0
+    if args.kv == "bf16":
+        pools = [(t16(kb), t16(vb))]
+        pools.append((pools[0][0].clone(), pools[0][1].clone()))
+    else:
+        # the FP8 cache is written by the library's own reshape_and_cache
+        from rllm_amd import ops
+        kv_code = rllm_amd.DTYPE_FP8_E4M3 if args.kv == "fp8_e4m3" else rllm_amd.DTYPE_FP8_E5M2
+        kf, vf = t16(kb), t16(vb)
+        top = 448.0 if kv_code == rllm_amd.DTYPE_FP8_E4M3 else 57344.0
+        k_scale, v_scale = float(kf.float().abs().max()) / top, float(vf.float().abs().max()) / top
+        slots = torch.arange(w.num_blocks * w.block_size, device=dev, dtype=torch.int64)
+        tok_k = kf.permute(0, 3, 1, 2).reshape(-1, w.num_kv_heads, w.head_dim).contiguous()
+        tok_v = vf.permute(0, 3, 1, 2).reshape(-1, w.num_kv_heads, w.head_dim).contiguous()
+        pools = []
+        for _ in range(2):
+            k8 = torch.empty(kf.shape, dtype=torch.uint8, device=dev)
+            v8 = torch.empty_like(k8)
+            ops.reshape_and_cache(tok_k, tok_v, k8, v8, slots, kv_dtype=kv_code, k_scale=k_scale, v_scale=v_scale)
+            pools.append((k8, v8))
+        del kf, vf, tok_k, tok_v
     bt = torch.from_numpy(w.block_tables).to(dev)
     sl = torch.from_numpy(w.seq_lens).to(dev)
     qsl = torch.from_numpy(w.query_start_loc()).to(dev)
@@ -124,7 +143,7 @@ def bench_prefill(args, w, lib, dev) -> int:
         kp, vp = pools[i & 1]
         rc = fn(out.data_ptr(), q.data_ptr(), kp.data_ptr(), vp.data_ptr(), bt.data_ptr(), sl.data_ptr(),
                 qsl.data_ptr(), w.num_seqs, T, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size,
-                w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, rllm_amd.DTYPE_BF16, 1.0, 1.0, sh)
+                w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, kv_code, k_scale, v_scale, sh)
         if rc:
             raise rllm_amd.KernelError(rc, "rllm_paged_attention_prefill_ex")
 
@@ -151,8 +170,10 @@ def bench_prefill(args, w, lib, dev) -> int:
         "value": round(flops / (ms_per_step * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1) (seeded), random permuted block tables",
-        "config": {"workload": w.name, "config_index": w.index, "num_seqs": w.num_seqs,
+        "vs_baseline": None, "dtype": "bf16" if args.kv == "bf16" else f"bf16 (KV {args.kv})",
+        "data": "synthetic N(0,1) (seeded), random permuted block tables",
+        "config": {"workload": w.name if args.kv == "bf16" else f"{w.name}_{args.kv}kv",
+                   "config_index": w.index, "num_seqs": w.num_seqs,
                    "num_tokens": T, "num_q_heads": w.num_q_heads, "num_kv_heads": w.num_kv_heads,
                    "head_dim": w.head_dim, "block_size": w.block_size,
                    "context_per_seq": int(w.seq_lens.max()), "parallelism": "single GPU"},
@@ -402,6 +423,9 @@ def main() -> int:
     ap.add_argument("--tp", type=int, default=1,
                     help="decode configs: time one GPU's share of a tensor-parallel run "
                          "(num_q_heads / tp and num_kv_heads / tp at the config's lengths)")
+    ap.add_argument("--kv", default="bf16", choices=["bf16", "fp8_e4m3", "fp8_e5m2"],
+                    help="config 5: KV cache dtype of the prefill line (FP8 written by the "
+                         "library's cache write, scales amax / max finite)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
