@@ -102,6 +102,27 @@ struct PrefillArgs {
     float v_scale;
 };
 
+// Two FP8 values (bytes 0-1 or 2-3 of w) -> two 16-bit values of the query
+// type, by the gfx950 scaled conversion with scale 1 (exact: every finite
+// E4M3 / E5M2 value is a bf16 and an f16 value).  Non-template wrappers, as
+// for the other target builtins.
+__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w, bool hi) {
+    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true))
+              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+}
+__device__ __forceinline__ uint32_t e5m2x2_to_bf16x2(uint32_t w, bool hi) {
+    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, true))
+              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, false));
+}
+__device__ __forceinline__ uint32_t e4m3x2_to_f16x2(uint32_t w, bool hi) {
+    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))
+              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+__device__ __forceinline__ uint32_t e5m2x2_to_f16x2(uint32_t w, bool hi) {
+    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true))
+              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false));
+}
+
 // 8 consecutive tokens of one cache row as 16-bit values (fp8 converted exactly)
 template <int QKIND, int KVKIND>
 __device__ __forceinline__ uint4 load8(const void* base, int64_t elem_off) {
@@ -111,16 +132,13 @@ __device__ __forceinline__ uint4 load8(const void* base, int64_t elem_off) {
         uint32_t d[4];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            f32x2 lo, hi;
-            if constexpr (KVKIND == KIND_FP8_E4M3) {
-                lo = __builtin_amdgcn_cvt_pk_f32_fp8(src[i], false);
-                hi = __builtin_amdgcn_cvt_pk_f32_fp8(src[i], true);
-            } else {
-                lo = __builtin_amdgcn_cvt_pk_f32_bf8(src[i], false);
-                hi = __builtin_amdgcn_cvt_pk_f32_bf8(src[i], true);
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                if constexpr (QKIND == KIND_BF16)
+                    d[2 * i + hf] = KVKIND == KIND_FP8_E4M3 ? e4m3x2_to_bf16x2(src[i], hf) : e5m2x2_to_bf16x2(src[i], hf);
+                else
+                    d[2 * i + hf] = KVKIND == KIND_FP8_E4M3 ? e4m3x2_to_f16x2(src[i], hf) : e5m2x2_to_f16x2(src[i], hf);
             }
-            d[2 * i] = Mfma<QKIND>::pack2_exact(lo.x, lo.y);
-            d[2 * i + 1] = Mfma<QKIND>::pack2_exact(hi.x, hi.y);
         }
         return make_uint4(d[0], d[1], d[2], d[3]);
     } else {

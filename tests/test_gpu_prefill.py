@@ -199,3 +199,26 @@ def test_prefill_invalid_arguments(dev):
     with pytest.raises(rllm_amd.KernelError):
         A.paged_attention_prefill_bf16(0, 0, 0, 0, 0, 0, 0, 1, 4, 8, 2, 128, 16, 4, 0.1)
     A.paged_attention_prefill_bf16(0, 0, 0, 0, 0, 0, 0, 1, 0, 8, 2, 128, 16, 4, 0.1)  # empty
+
+
+@pytest.mark.parametrize("fp8", [O.FP8_E4M3, O.FP8_E5M2])
+@pytest.mark.parametrize("q_kind", [O.BF16, O.F16])
+def test_prefill_fp8_every_byte_converts_exactly(dev, fp8, q_kind):
+    """One query over one cached token makes the output equal the converted V
+    row: every finite FP8 byte, through the FP8 staging path, must come out as
+    its exact value in the query's 16-bit type (all of them are representable)."""
+    bytes_ = np.arange(256, dtype=np.uint8)
+    dec = O.decode(bytes_, fp8)
+    bytes_ = np.where(np.isfinite(dec), bytes_, 0).astype(np.uint8)
+    D, B = 128, 2
+    vb = np.zeros((B, 1, D, 16), np.uint8)
+    vb[:, 0, :, 0] = bytes_.reshape(B, D)
+    kb = np.zeros_like(vb)
+    bt = np.arange(B, dtype=np.int32).reshape(B, 1)
+    sl = np.ones(B, np.int32)
+    qsl = np.arange(B + 1, dtype=np.int32)
+    qb = O.encode(np.ones((B, 1, D), np.float32), q_kind)
+    log_case(f"prefill all fp8 bytes fp8={fp8} q={q_kind}")
+    got = run_prefill(dev, qb, q_kind, kb, vb, fp8, bt, sl, qsl, 0.1)
+    want = O.decode(bytes_, fp8).reshape(B, D)
+    assert np.array_equal(got[:, 0, :], want)
