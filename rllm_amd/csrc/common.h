@@ -156,6 +156,26 @@ __host__ __device__ __forceinline__ uint8_t fp8_e5m2_encode_rne(float x) {
     return static_cast<uint8_t>(sign | fp8_round_nearest<2, 15>(a));
 }
 
+// Two FP8 values (bytes 0-1 or 2-3 of w) -> two packed bf16 / f16 values, by the gfx950 scaled conversion with scale 1 (exact: every finite
+// E4M3 / E5M2 value is a bf16 and an f16 value).  Non-template wrappers, as
+// for the other target builtins.
+__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w, bool hi) {
+    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true))
+              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+}
+__device__ __forceinline__ uint32_t e5m2x2_to_bf16x2(uint32_t w, bool hi) {
+    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, true))
+              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, false));
+}
+__device__ __forceinline__ uint32_t e4m3x2_to_f16x2(uint32_t w, bool hi) {
+    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))
+              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+__device__ __forceinline__ uint32_t e5m2x2_to_f16x2(uint32_t w, bool hi) {
+    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true))
+              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false));
+}
+
 // ---------------------------------------------------------------------------
 // wave64 helpers
 // ---------------------------------------------------------------------------

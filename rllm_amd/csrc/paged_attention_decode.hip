@@ -77,10 +77,6 @@ template <> struct Dot<KIND_BF16> {
     __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){lo, hi}, bf16x2_t));
     }
-    // exact for values with <= 8 significant bits (decoded fp8)
-    __device__ __forceinline__ static uint32_t pack_exact(float lo, float hi) {
-        return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-    }
     __device__ __forceinline__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
     __device__ __forceinline__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 };
@@ -92,7 +88,6 @@ template <> struct Dot<KIND_F16> {
     __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){lo, hi}, f16x2_t));
     }
-    __device__ __forceinline__ static uint32_t pack_exact(float lo, float hi) { return pack(lo, hi); }
     __device__ __forceinline__ static float lo(uint32_t w) { return f16_lo(w); }
     __device__ __forceinline__ static float hi(uint32_t w) { return f16_hi(w); }
 };
@@ -132,16 +127,13 @@ __device__ __forceinline__ void seg_words(const typename Seg<KVKIND>::raw& r, ui
         const uint32_t src[2] = {r.x, r.y};
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            float2_t a, b;
-            if constexpr (KVKIND == KIND_FP8_E4M3) {
-                a = __builtin_amdgcn_cvt_pk_f32_fp8(src[i], false);
-                b = __builtin_amdgcn_cvt_pk_f32_fp8(src[i], true);
-            } else {
-                a = __builtin_amdgcn_cvt_pk_f32_bf8(src[i], false);
-                b = __builtin_amdgcn_cvt_pk_f32_bf8(src[i], true);
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                if constexpr (QKIND == KIND_BF16)
+                    w[2 * i + hf] = KVKIND == KIND_FP8_E4M3 ? e4m3x2_to_bf16x2(src[i], hf) : e5m2x2_to_bf16x2(src[i], hf);
+                else
+                    w[2 * i + hf] = KVKIND == KIND_FP8_E4M3 ? e4m3x2_to_f16x2(src[i], hf) : e5m2x2_to_f16x2(src[i], hf);
             }
-            w[2 * i] = Dot<QKIND>::pack_exact(a.x, a.y);
-            w[2 * i + 1] = Dot<QKIND>::pack_exact(b.x, b.y);
         }
     }
 }

@@ -70,10 +70,6 @@ template <> struct Mfma<KIND_BF16> {
     __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
     }
-    // exact conversion of an fp8 value (<= 4 significant bits) to 16-bit
-    __device__ __forceinline__ static uint32_t pack2_exact(float lo, float hi) {
-        return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
-    }
 };
 template <> struct Mfma<KIND_F16> {
     using vec = f16x8;
@@ -83,9 +79,6 @@ template <> struct Mfma<KIND_F16> {
     __device__ __forceinline__ static uint16_t bits(float f) { return f32_to_f16_bits(f); }
     __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
-    }
-    __device__ __forceinline__ static uint32_t pack2_exact(float lo, float hi) {
-        return static_cast<uint32_t>(f32_to_f16_bits(lo)) | (static_cast<uint32_t>(f32_to_f16_bits(hi)) << 16);
     }
 };
 
@@ -101,27 +94,6 @@ struct PrefillArgs {
     float s_scale;   // scale * log2(e) * k_scale
     float v_scale;
 };
-
-// Two FP8 values (bytes 0-1 or 2-3 of w) -> two 16-bit values of the query
-// type, by the gfx950 scaled conversion with scale 1 (exact: every finite
-// E4M3 / E5M2 value is a bf16 and an f16 value).  Non-template wrappers, as
-// for the other target builtins.
-__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w, bool hi) {
-    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true))
-              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
-}
-__device__ __forceinline__ uint32_t e5m2x2_to_bf16x2(uint32_t w, bool hi) {
-    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, true))
-              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, false));
-}
-__device__ __forceinline__ uint32_t e4m3x2_to_f16x2(uint32_t w, bool hi) {
-    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))
-              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
-}
-__device__ __forceinline__ uint32_t e5m2x2_to_f16x2(uint32_t w, bool hi) {
-    return hi ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true))
-              : __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false));
-}
 
 // 8 consecutive tokens of one cache row as 16-bit values (fp8 converted exactly)
 template <int QKIND, int KVKIND>
