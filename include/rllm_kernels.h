@@ -333,6 +333,19 @@ int32_t rllm_rope_cache_write(void *q_out, const void *q, const void *k, const v
                               int64_t num_blocks, int64_t max_position, int32_t dtype,
                               int32_t kv_dtype, float k_scale, float v_scale, uintptr_t stream);
 
+/* New: rllm_rope_cache_write with a choice of FP8 rounding (fp8_rounding is
+ * RLLM_FP8_ROUND_TOWARD_ZERO, which rllm_rope_cache_write uses, or
+ * RLLM_FP8_ROUND_NEAREST_EVEN; see rllm_cache_write_fp8_ex).  Ignored for
+ * 16-bit caches. */
+int32_t rllm_rope_cache_write_ex(void *q_out, const void *q, const void *k, const void *v,
+                                 void *key_cache, void *value_cache, const int64_t *slot_mapping,
+                                 const int32_t *positions, const float *cos_cache,
+                                 const float *sin_cache, int64_t num_tokens, int64_t num_q_heads,
+                                 int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+                                 int64_t num_blocks, int64_t max_position, int32_t dtype,
+                                 int32_t kv_dtype, float k_scale, float v_scale,
+                                 int32_t fp8_rounding, uintptr_t stream);
+
 /* New (additive), host only: fills the f32 cos / sin tables
  * [max_position, head_dim/2] that rllm_rope_cache_write reads, as
  * RotaryEmbedding::new computes them (rope.rs:13-33: f64 angles, f32 store).

@@ -77,6 +77,8 @@ def lib() -> ctypes.CDLL:
     L.orc_rope_cache_build.argtypes = [P, P, i64, i64, c.c_float]
     L.orc_rope_cache_write.argtypes = [P, P, P, P, P, P, P, P, P, P, i64, i64, i64, i64, i64,
                                        i64, i64, c.c_int, c.c_int, c.c_float, c.c_float]
+    L.orc_rope_cache_write_rounded.argtypes = [P, P, P, P, P, P, P, P, P, P, i64, i64, i64, i64, i64,
+                                               i64, i64, c.c_int, c.c_int, c.c_float, c.c_float, c.c_int]
     L.orc_paged_attention_decode.argtypes = [P, P, c.c_int, P, P, c.c_int, P, P, i64, i64, i64,
                                              i64, i64, i64, c.c_float, c.c_float, c.c_float,
                                              c.c_int, c.c_int]
@@ -220,9 +222,11 @@ def rope_cache_build(max_position: int, head_dim: int, theta: float = 10000.0):
 
 
 def rope_cache_write(q, k, v, key_cache, value_cache, slot_mapping, positions, cos, sin,
-                     in_kind: int, cache_kind: int, k_scale: float = 1.0, v_scale: float = 1.0):
+                     in_kind: int, cache_kind: int, k_scale: float = 1.0, v_scale: float = 1.0,
+                     round_nearest: bool = False):
     """Rotate q (returned) and k in the activation dtype, then write the rotated
-    key and v into the numpy caches [nb, Hkv, D, bs] in place."""
+    key and v into the numpy caches [nb, Hkv, D, bs] in place (FP8 rounded
+    toward zero, or to nearest even with ``round_nearest``)."""
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
     v = np.ascontiguousarray(v, dtype=np.uint16)
@@ -234,9 +238,10 @@ def rope_cache_write(q, k, v, key_cache, value_cache, slot_mapping, positions, c
     cos = np.ascontiguousarray(cos, dtype=np.float32)
     sin = np.ascontiguousarray(sin, dtype=np.float32)
     q_out = np.empty_like(q)
-    lib().orc_rope_cache_write(_p(q_out), _p(q), _p(k), _p(v), _p(key_cache), _p(value_cache),
-                               _p(sm), _p(pos), _p(cos), _p(sin), T, hq, hkv, d, bs, nb,
-                               cos.shape[0], in_kind, cache_kind, k_scale, v_scale)
+    lib().orc_rope_cache_write_rounded(_p(q_out), _p(q), _p(k), _p(v), _p(key_cache), _p(value_cache),
+                                       _p(sm), _p(pos), _p(cos), _p(sin), T, hq, hkv, d, bs, nb,
+                                       cos.shape[0], in_kind, cache_kind, k_scale, v_scale,
+                                       1 if round_nearest else 0)
     return q_out
 
 

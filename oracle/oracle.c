@@ -569,6 +569,20 @@ void orc_rope_cache_write(uint16_t *q_out, const uint16_t *q, const uint16_t *k,
                           int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                           int64_t block_size, int64_t num_blocks, int64_t max_position,
                           int in_kind, int cache_kind, float k_scale, float v_scale) {
+    orc_rope_cache_write_rounded(q_out, q, k, v, key_cache, value_cache, slot_mapping, positions,
+                                 cos_cache, sin_cache, num_tokens, num_q_heads, num_kv_heads,
+                                 head_dim, block_size, num_blocks, max_position, in_kind,
+                                 cache_kind, k_scale, v_scale, 0);
+}
+
+void orc_rope_cache_write_rounded(uint16_t *q_out, const uint16_t *q, const uint16_t *k,
+                                  const uint16_t *v, void *key_cache, void *value_cache,
+                                  const int64_t *slot_mapping, const int32_t *positions,
+                                  const float *cos_cache, const float *sin_cache,
+                                  int64_t num_tokens, int64_t num_q_heads, int64_t num_kv_heads,
+                                  int64_t head_dim, int64_t block_size, int64_t num_blocks,
+                                  int64_t max_position, int in_kind, int cache_kind,
+                                  float k_scale, float v_scale, int round_nearest) {
     const int64_t half = head_dim / 2;
     uint16_t *krot = (uint16_t *)malloc((size_t)(num_kv_heads * head_dim) * sizeof(uint16_t));
     for (int64_t t = 0; t < num_tokens; t++) {
@@ -583,9 +597,9 @@ void orc_rope_cache_write(uint16_t *q_out, const uint16_t *q, const uint16_t *k,
             rope_row(k + (t * num_kv_heads + h) * head_dim, krot + h * head_dim, cs, sn, head_dim,
                      in_kind);
         /* the rotated key and the value go through the cache write */
-        orc_cache_write(key_cache, value_cache, krot, v + t * num_kv_heads * head_dim,
-                        slot_mapping + t, 1, num_kv_heads, head_dim, block_size, num_blocks,
-                        in_kind, cache_kind, k_scale, v_scale);
+        orc_cache_write_rounded(key_cache, value_cache, krot, v + t * num_kv_heads * head_dim,
+                                slot_mapping + t, 1, num_kv_heads, head_dim, block_size, num_blocks,
+                                in_kind, cache_kind, k_scale, v_scale, round_nearest);
     }
     free(krot);
 }

@@ -144,6 +144,15 @@ void orc_rope_cache_write(uint16_t *q_out, const uint16_t *q, const uint16_t *k,
                           int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                           int64_t block_size, int64_t num_blocks, int64_t max_position,
                           int in_kind, int cache_kind, float k_scale, float v_scale);
+/* As orc_rope_cache_write; round_nearest selects the nearest-even FP8 encoders. */
+void orc_rope_cache_write_rounded(uint16_t *q_out, const uint16_t *q, const uint16_t *k,
+                                  const uint16_t *v, void *key_cache, void *value_cache,
+                                  const int64_t *slot_mapping, const int32_t *positions,
+                                  const float *cos_cache, const float *sin_cache,
+                                  int64_t num_tokens, int64_t num_q_heads, int64_t num_kv_heads,
+                                  int64_t head_dim, int64_t block_size, int64_t num_blocks,
+                                  int64_t max_position, int in_kind, int cache_kind,
+                                  float k_scale, float v_scale, int round_nearest);
 
 /* ---- decode paged attention ------------------------------------------ */
 /* out: [num_seqs, num_q_heads, head_dim] float32.

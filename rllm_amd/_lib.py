@@ -68,6 +68,8 @@ SIGNATURES = {
     "rllm_cache_write_fp8_ex": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _F, _F, _I32, _I32, _U],
     "rllm_rope_cache_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                               _I64, _I64, _I32, _I32, _F, _F, _U],
+    "rllm_rope_cache_write_ex": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                                 _I64, _I64, _I32, _I32, _F, _F, _I32, _U],
     "rllm_rope_tables": [_P, _P, _I64, _I64, _F],
     "rllm_cache_copy_blocks": [_P, _P, _I64, _P, _I64, _I64, _I64, _U],
     "rllm_cache_swap_out": [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _U],

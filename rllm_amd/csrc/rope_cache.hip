@@ -73,11 +73,13 @@ __device__ __forceinline__ uint4 pack8(const uint16_t (&e)[8]) {
 }
 
 // one cache element: 16-bit caches store the bits, FP8 caches encode x / scale
-template <int IN_KIND, int CACHE_KIND, bool DIV>
+// rounding toward zero (the reference contract) or, with RNE, to nearest even
+template <int IN_KIND, int CACHE_KIND, bool DIV, bool RNE>
 __device__ __forceinline__ uint8_t enc8(uint16_t bits, float scale) {
     // scale is the divisor, or its exact reciprocal when it is a power of two
     const float x = DIV ? dec16<IN_KIND>(bits) / scale : dec16<IN_KIND>(bits) * scale;
-    return CACHE_KIND == KIND_FP8_E4M3 ? fp8_e4m3_encode(x) : fp8_e5m2_encode(x);
+    if constexpr (RNE) return CACHE_KIND == KIND_FP8_E4M3 ? fp8_e4m3_encode_rne(x) : fp8_e5m2_encode_rne(x);
+    else return CACHE_KIND == KIND_FP8_E4M3 ? fp8_e4m3_encode(x) : fp8_e5m2_encode(x);
 }
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -159,7 +161,7 @@ __device__ __forceinline__ int32_t clamp_pos(int32_t p, int32_t max_position) {
 // rotated k and v staged in LDS as [token][D + 8], then written as cache rows;
 // r >= Hkv: the q rotations of token r - Hkv (uniform position and cos / sin
 // row; lanes beyond Hq * D / 16 items idle).
-template <int IN_KIND, int CACHE_KIND, bool DIV>
+template <int IN_KIND, int CACHE_KIND, bool DIV, bool RNE>
 __global__ __launch_bounds__(ROPE_THREADS) void rope_cache_kernel(
     uint16_t* q_out, const uint16_t* q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, void* __restrict__ key_cache, void* __restrict__ value_cache,
@@ -268,10 +270,10 @@ __global__ __launch_bounds__(ROPE_THREADS) void rope_cache_kernel(
                 uint32_t w[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    w[i] = static_cast<uint32_t>(enc8<IN_KIND, CACHE_KIND, DIV>(e[4 * i], sc)) |
-                           (static_cast<uint32_t>(enc8<IN_KIND, CACHE_KIND, DIV>(e[4 * i + 1], sc)) << 8) |
-                           (static_cast<uint32_t>(enc8<IN_KIND, CACHE_KIND, DIV>(e[4 * i + 2], sc)) << 16) |
-                           (static_cast<uint32_t>(enc8<IN_KIND, CACHE_KIND, DIV>(e[4 * i + 3], sc)) << 24);
+                    w[i] = static_cast<uint32_t>(enc8<IN_KIND, CACHE_KIND, DIV, RNE>(e[4 * i], sc)) |
+                           (static_cast<uint32_t>(enc8<IN_KIND, CACHE_KIND, DIV, RNE>(e[4 * i + 1], sc)) << 8) |
+                           (static_cast<uint32_t>(enc8<IN_KIND, CACHE_KIND, DIV, RNE>(e[4 * i + 2], sc)) << 16) |
+                           (static_cast<uint32_t>(enc8<IN_KIND, CACHE_KIND, DIV, RNE>(e[4 * i + 3], sc)) << 24);
                 *reinterpret_cast<uint4*>(static_cast<uint8_t*>(cache) + idx) = make_uint4(w[0], w[1], w[2], w[3]);
             }
         } else {
@@ -282,7 +284,7 @@ __global__ __launch_bounds__(ROPE_THREADS) void rope_cache_kernel(
                 if constexpr (CACHE_KIND == KIND_F16 || CACHE_KIND == KIND_BF16)
                     static_cast<uint16_t*>(cache)[base + hd] = x;
                 else
-                    static_cast<uint8_t*>(cache)[base + hd] = enc8<IN_KIND, CACHE_KIND, DIV>(x, sc);
+                    static_cast<uint8_t*>(cache)[base + hd] = enc8<IN_KIND, CACHE_KIND, DIV, RNE>(x, sc);
             }
         }
     }
@@ -316,41 +318,47 @@ struct RopeArgs {
     int32_t roles;
 };
 
-template <int IN_KIND, int CACHE_KIND>
+template <int IN_KIND, int CACHE_KIND, bool RNE = false>
 int32_t launch_rope(dim3 grid, hipStream_t st, const RopeArgs& a) {
     constexpr bool fp8 = CACHE_KIND == KIND_FP8_E4M3 || CACHE_KIND == KIND_FP8_E5M2;
     const size_t lds = 2u * ROPE_GROUP * (a.d + 8) * sizeof(uint16_t);
     if (fp8 && !(pow2(a.ks) && pow2(a.vs)))
-        hipLaunchKernelGGL((rope_cache_kernel<IN_KIND, CACHE_KIND, true>), grid, dim3(ROPE_THREADS), lds, st,
+        hipLaunchKernelGGL((rope_cache_kernel<IN_KIND, CACHE_KIND, true, RNE>), grid, dim3(ROPE_THREADS), lds, st,
                            a.q_out, a.q, a.k, a.v, a.kc, a.vc, a.sm, a.pos, a.cs, a.sn, a.n, a.hq, a.hkv, a.d,
                            a.bs, a.nb, a.maxp, a.ks, a.vs, a.roles);
     else
-        hipLaunchKernelGGL((rope_cache_kernel<IN_KIND, CACHE_KIND, false>), grid, dim3(ROPE_THREADS), lds, st,
+        hipLaunchKernelGGL((rope_cache_kernel<IN_KIND, CACHE_KIND, false, RNE>), grid, dim3(ROPE_THREADS), lds, st,
                            a.q_out, a.q, a.k, a.v, a.kc, a.vc, a.sm, a.pos, a.cs, a.sn, a.n, a.hq, a.hkv, a.d,
                            a.bs, a.nb, a.maxp, fp8 ? 1.0f / a.ks : 1.0f, fp8 ? 1.0f / a.vs : 1.0f, a.roles);
     return launch_status();
 }
 
 template <int IN_KIND>
-int32_t dispatch_cache(int32_t kv_dtype, dim3 grid, hipStream_t st, const RopeArgs& a) {
+int32_t dispatch_cache(int32_t kv_dtype, bool rne, dim3 grid, hipStream_t st, const RopeArgs& a) {
     switch (kv_dtype) {
-        case KIND_FP8_E4M3: return launch_rope<IN_KIND, KIND_FP8_E4M3>(grid, st, a);
-        case KIND_FP8_E5M2: return launch_rope<IN_KIND, KIND_FP8_E5M2>(grid, st, a);
+        case KIND_FP8_E4M3:
+            return rne ? launch_rope<IN_KIND, KIND_FP8_E4M3, true>(grid, st, a)
+                       : launch_rope<IN_KIND, KIND_FP8_E4M3>(grid, st, a);
+        case KIND_FP8_E5M2:
+            return rne ? launch_rope<IN_KIND, KIND_FP8_E5M2, true>(grid, st, a)
+                       : launch_rope<IN_KIND, KIND_FP8_E5M2>(grid, st, a);
         default: return launch_rope<IN_KIND, IN_KIND>(grid, st, a);
     }
 }
 
 }  // namespace
 
-extern "C" int32_t rllm_rope_cache_write(void* q_out, const void* q, const void* k, const void* v,
-                                         void* key_cache, void* value_cache,
-                                         const int64_t* slot_mapping, const int32_t* positions,
-                                         const float* cos_cache, const float* sin_cache,
-                                         int64_t num_tokens, int64_t num_q_heads,
-                                         int64_t num_kv_heads, int64_t head_dim,
-                                         int64_t block_size, int64_t num_blocks,
-                                         int64_t max_position, int32_t dtype, int32_t kv_dtype,
-                                         float k_scale, float v_scale, uintptr_t stream) {
+extern "C" int32_t rllm_rope_cache_write_ex(void* q_out, const void* q, const void* k, const void* v,
+                                            void* key_cache, void* value_cache,
+                                            const int64_t* slot_mapping, const int32_t* positions,
+                                            const float* cos_cache, const float* sin_cache,
+                                            int64_t num_tokens, int64_t num_q_heads,
+                                            int64_t num_kv_heads, int64_t head_dim,
+                                            int64_t block_size, int64_t num_blocks,
+                                            int64_t max_position, int32_t dtype, int32_t kv_dtype,
+                                            float k_scale, float v_scale, int32_t fp8_rounding,
+                                            uintptr_t stream) {
+    RLLM_CHECK_ARG(fp8_rounding == RLLM_FP8_ROUND_TOWARD_ZERO || fp8_rounding == RLLM_FP8_ROUND_NEAREST_EVEN);
     if (num_tokens == 0) return 0;
     RLLM_CHECK_ARG(num_tokens > 0 && num_tokens <= (int64_t(1) << 31) - 1);
     RLLM_CHECK_ARG(dtype == RLLM_DTYPE_F16 || dtype == RLLM_DTYPE_BF16);
@@ -380,8 +388,24 @@ extern "C" int32_t rllm_rope_cache_write(void* q_out, const void* q, const void*
                      (int32_t)num_kv_heads, (int32_t)head_dim, block_size, num_blocks, (int32_t)max_position,
                      k_scale, v_scale, (int32_t)(num_kv_heads + q_slices)};
     hipStream_t st = as_stream(stream);
-    if (dtype == RLLM_DTYPE_BF16) return dispatch_cache<KIND_BF16>(kv_dtype, grid, st, a);
-    return dispatch_cache<KIND_F16>(kv_dtype, grid, st, a);
+    const bool rne = fp8_rounding == RLLM_FP8_ROUND_NEAREST_EVEN;
+    if (dtype == RLLM_DTYPE_BF16) return dispatch_cache<KIND_BF16>(kv_dtype, rne, grid, st, a);
+    return dispatch_cache<KIND_F16>(kv_dtype, rne, grid, st, a);
+}
+
+extern "C" int32_t rllm_rope_cache_write(void* q_out, const void* q, const void* k, const void* v,
+                                         void* key_cache, void* value_cache,
+                                         const int64_t* slot_mapping, const int32_t* positions,
+                                         const float* cos_cache, const float* sin_cache,
+                                         int64_t num_tokens, int64_t num_q_heads,
+                                         int64_t num_kv_heads, int64_t head_dim,
+                                         int64_t block_size, int64_t num_blocks,
+                                         int64_t max_position, int32_t dtype, int32_t kv_dtype,
+                                         float k_scale, float v_scale, uintptr_t stream) {
+    return rllm_rope_cache_write_ex(q_out, q, k, v, key_cache, value_cache, slot_mapping, positions, cos_cache,
+                                    sin_cache, num_tokens, num_q_heads, num_kv_heads, head_dim, block_size,
+                                    num_blocks, max_position, dtype, kv_dtype, k_scale, v_scale,
+                                    RLLM_FP8_ROUND_TOWARD_ZERO, stream);
 }
 
 // Host-side table builder (no GPU work): RotaryEmbedding::new

@@ -468,11 +468,12 @@ inline Result<void> rope_cache_write(void* q_out, const void* q, const void* k, 
                                      const float* cos_cache, const float* sin_cache, int64_t num_tokens,
                                      int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
                                      int64_t num_blocks, int64_t max_position, DType dtype, DType kv_dtype,
-                                     float k_scale, float v_scale, uintptr_t stream) {
-    return check(rllm_rope_cache_write(q_out, q, k, v, key_cache, value_cache, slot_mapping, positions, cos_cache,
-                                       sin_cache, num_tokens, num_q_heads, num_kv_heads, head_dim, block_size,
-                                       num_blocks, max_position, abi_dtype(dtype), abi_dtype(kv_dtype),
-                                       k_scale, v_scale, stream));
+                                     float k_scale, float v_scale, uintptr_t stream,
+                                     int32_t fp8_rounding = RLLM_FP8_ROUND_TOWARD_ZERO) {
+    return check(rllm_rope_cache_write_ex(q_out, q, k, v, key_cache, value_cache, slot_mapping, positions,
+                                          cos_cache, sin_cache, num_tokens, num_q_heads, num_kv_heads, head_dim,
+                                          block_size, num_blocks, max_position, abi_dtype(dtype),
+                                          abi_dtype(kv_dtype), k_scale, v_scale, fp8_rounding, stream));
 }
 
 // ---------------------------------------------------------------------------

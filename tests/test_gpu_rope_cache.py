@@ -8,6 +8,7 @@ import torch
 
 import oracle as O
 from gpu_util import bits16, log_case, t16, t8, ti
+import rllm_amd
 from rllm_amd import KernelError
 from rllm_amd import ops
 
@@ -47,7 +48,7 @@ def _host_cache(t):
 
 
 def _run(dev, T, hq, hkv, D, nb, bs, kind, cache_kind, ks=1.0, vs=1.0, P=4096, theta=10000.0,
-         seed=0, inplace=False, scale=1.0, slots=None, pos=None):
+         seed=0, inplace=False, scale=1.0, slots=None, pos=None, rne=False):
     q, k, v, kc, vc, rslots, rpos = _case(seed, T, hq, hkv, D, nb, bs, kind, cache_kind, P, scale)
     slots = rslots if slots is None else np.asarray(slots, np.int64)
     pos = rpos if pos is None else np.asarray(pos, np.int32)
@@ -55,10 +56,11 @@ def _run(dev, T, hq, hkv, D, nb, bs, kind, cache_kind, ks=1.0, vs=1.0, P=4096, t
     eq = q.copy() if hq else None
     ek, ev = kc.copy(), vc.copy()
     if hq:
-        eq = O.rope_cache_write(q, k, v, ek, ev, slots, pos, cos, sin, kind, cache_kind, ks, vs)
+        eq = O.rope_cache_write(q, k, v, ek, ev, slots, pos, cos, sin, kind, cache_kind, ks, vs,
+                                round_nearest=rne)
     else:
         O.rope_cache_write(np.zeros((T, 0, D), np.uint16), k, v, ek, ev, slots, pos, cos, sin,
-                           kind, cache_kind, ks, vs)
+                           kind, cache_kind, ks, vs, round_nearest=rne)
     dt = DT[kind]
     gq = t16(q, dt, dev) if hq else None
     gk, gv = t16(k, dt, dev), t16(v, dt, dev)
@@ -69,7 +71,8 @@ def _run(dev, T, hq, hkv, D, nb, bs, kind, cache_kind, ks=1.0, vs=1.0, P=4096, t
              f"scales=({ks},{vs}) inplace={inplace}")
     out = ops.rope_and_cache(gq, gk, gv, gkc, gvc, ti(slots, torch.int64, dev),
                              ti(pos, torch.int32, dev), cc, sc, q_out=gq if inplace else None,
-                             kv_dtype=kvd, k_scale=ks, v_scale=vs)
+                             kv_dtype=kvd, k_scale=ks, v_scale=vs,
+                             fp8_rounding=rllm_amd.FP8_ROUND_NEAREST_EVEN if rne else rllm_amd.FP8_ROUND_TOWARD_ZERO)
     torch.cuda.synchronize()
     if hq:
         assert np.array_equal(bits16(out), eq), "rotated q differs"
@@ -92,6 +95,13 @@ def test_rope_cache_fp8_scales(dev, ks, vs):
     # power-of-two scales take the reciprocal multiply, others the division
     _run(dev, 48, 8, 2, 64, 20, 16, O.BF16, O.FP8_E4M3, ks, vs, seed=2)
     _run(dev, 48, 8, 2, 64, 20, 16, O.F16, O.FP8_E5M2, ks, vs, seed=3)
+
+
+@pytest.mark.parametrize("ks,vs", [(0.5, 2.0), (0.0117, 0.37)])
+@pytest.mark.parametrize("kind,cache", [(O.BF16, O.FP8_E4M3), (O.F16, O.FP8_E5M2), (O.BF16, O.FP8_E5M2)])
+def test_rope_cache_fp8_nearest_even(dev, ks, vs, kind, cache):
+    # rllm_rope_cache_write_ex with nearest-even FP8 bytes, bit-exact
+    _run(dev, 64, 32, 8, 128, 80, 16, kind, cache, ks, vs, seed=4, rne=True)
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 1, 16, 1, 1), (37, 12, 4, 80, 9, 32), (5, 4, 4, 256, 3, 8),
