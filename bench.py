@@ -262,6 +262,111 @@ def bench_rope_cache(args, w, lib, dev) -> int:
     return 0
 
 
+def bench_decode_step(args, w, lib, dev) -> int:
+    """--op decode_step: one attention layer's decode step of config w (fused
+    RoPE + cache write of each sequence's new token, then decode attention
+    over the updated cache), launched eagerly and replayed from a hipGraph
+    captured once (torch.cuda.CUDAGraph around the same C-ABI calls; the
+    caller workspace is allocated before capture).  Reports microseconds per
+    step both ways; the steps run back to back between one event pair."""
+    import numpy as np
+    import torch
+
+    import rllm_amd
+    from rllm_amd import attention as A
+    from rllm_amd import ops, workloads
+    if w.kv_dtype != "bf16" or w.index == 5:
+        print("--op decode_step runs the bf16 decode configs (1, 2, 4, 6)", file=sys.stderr)
+        return 2
+    B, hq, hkv, D, bs = w.num_seqs, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size
+    qb, kb, vb = workloads.host_tensors(w)
+    t16 = lambda b: torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(dev)
+    q, kc, vc = t16(qb), t16(kb), t16(vb)
+    g = torch.Generator(device="cpu").manual_seed(w.index)
+    nk = torch.randn(B, hkv, D, generator=g).to(torch.bfloat16).to(dev)
+    nv = torch.randn(B, hkv, D, generator=g).to(torch.bfloat16).to(dev)
+    slots = torch.from_numpy(w.new_token_slots()).to(dev)
+    pos = torch.from_numpy(w.new_token_positions()).to(dev)
+    max_pos = int(w.seq_lens.max())
+    cos, sin = ops.rope_cache_tables(max_pos, D, 500000.0, device=dev)
+    bt = torch.from_numpy(w.block_tables).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    out = torch.empty_like(q)
+    ws_bytes = A.decode_workspace_size(B, hq, hkv, D, bs, w.max_blocks, 0)
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    ops.validate_tables(bt, sl, w.num_blocks, bs)
+    rope, dec = lib.rllm_rope_cache_write, lib.rllm_paged_attention_decode_ex
+
+    def launch(sh):
+        rc = rope(q.data_ptr(), q.data_ptr(), nk.data_ptr(), nv.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                  slots.data_ptr(), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, hq, hkv, D, bs,
+                  w.num_blocks, max_pos, rllm_amd.DTYPE_BF16, rllm_amd.DTYPE_BF16, 1.0, 1.0, sh)
+        if rc:
+            raise rllm_amd.KernelError(rc, "rllm_rope_cache_write")
+        rc = dec(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                 B, hq, hkv, D, bs, w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, rllm_amd.DTYPE_BF16, 1.0, 1.0,
+                 0, ws.data_ptr(), ws.numel(), sh)
+        if rc:
+            raise rllm_amd.KernelError(rc, "rllm_paged_attention_decode_ex")
+
+    stream = torch.cuda.current_stream()
+    sh = int(stream.cuda_stream)
+    for _ in range(args.warmup):
+        launch(sh)
+    torch.cuda.synchronize()
+
+    def timed(fn):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        for _ in range(args.steps):
+            fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / args.steps, ev0.elapsed_time(ev1) / args.steps
+
+    eager_wall, eager_ms = timed(lambda: launch(sh))
+
+    def launch_py():   # the same two calls through the Python wrappers (their checks run on the CPU)
+        ops.rope_and_cache(q, nk, nv, kc, vc, slots, pos, cos, sin, q_out=q)
+        ops.paged_decode(q, kc, vc, bt, sl, w.scale, out=out, workspace=ws, validate=False)
+
+    py_wall, py_ms = timed(launch_py)
+    cs = torch.cuda.Stream()
+    cs.wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cs):
+        launch(int(cs.cuda_stream))   # warm the capture stream's workspace state
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=cs):
+            launch(int(cs.cuda_stream))
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_wall, graph_ms = timed(graph.replay)
+    nbytes = w.decode_bytes() + w.rope_cache_bytes()
+    res = {
+        "metric": "decode layer step (fused RoPE + cache write + decode attention) us, eager and hipGraph",
+        "value": round(graph_ms * 1e3, 2), "unit": "us/step (graph replay)", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(graph_wall, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1) (seeded), random permuted block tables",
+        "config": {"workload": w.name, "config_index": w.index, "op": "decode_step", "num_seqs": B,
+                   "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": D, "parallelism": "single GPU"},
+        "eager_us_per_step": round(eager_ms * 1e3, 2), "eager_wall_us_per_step": round(eager_wall * 1e3, 2),
+        "eager_python_wrappers_us_per_step": round(py_ms * 1e3, 2),
+        "graph_us_per_step": round(graph_ms * 1e3, 2), "graph_wall_us_per_step": round(graph_wall * 1e3, 2),
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / (graph_ms * 1e-3) / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(nbytes / (graph_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": nbytes},
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def bench_block_moves(args, w, lib, dev) -> int:
     """--op copy_blocks / swap_out / swap_in: block-list data movement over a
     32-layer cache with config w's block geometry (Llama-3-8B: 8 kv heads x
@@ -415,10 +520,11 @@ def main() -> int:
                     help="benchmark config: 2 (default) is the headline decode line; 5 is chunked prefill")
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
     ap.add_argument("--op", default="attention",
-                    choices=["attention", "rope_cache", "copy_blocks", "swap_out", "swap_in", "rmsnorm",
-                             "silu_mul"],
+                    choices=["attention", "rope_cache", "decode_step", "copy_blocks", "swap_out", "swap_in",
+                             "rmsnorm", "silu_mul"],
                     help="attention (default): the config's decode or prefill line; rope_cache: the fused "
-                         "RoPE + cache write over the config's new tokens; copy_blocks / swap_out / swap_in: "
+                         "RoPE + cache write over the config's new tokens; decode_step: RoPE + cache write + "
+                         "decode attention, eager and replayed from a hipGraph; copy_blocks / swap_out / swap_in: "
                          "block-list moves over a 32-layer cache; rmsnorm / silu_mul: at Llama-3-8B widths")
     ap.add_argument("--tp", type=int, default=1,
                     help="decode configs: time one GPU's share of a tensor-parallel run "
@@ -447,6 +553,8 @@ def main() -> int:
     w = workloads.config(args.config)
     if args.op == "rope_cache":
         return bench_rope_cache(args, w, lib, dev)
+    if args.op == "decode_step":
+        return bench_decode_step(args, w, lib, dev)
     if args.op in ("copy_blocks", "swap_out", "swap_in"):
         return bench_block_moves(args, w, lib, dev)
     if args.op in ("rmsnorm", "silu_mul"):
