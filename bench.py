@@ -520,10 +520,12 @@ def main() -> int:
                     help="benchmark config: 2 (default) is the headline decode line; 5 is chunked prefill")
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
     ap.add_argument("--op", default="attention",
-                    choices=["attention", "rope_cache", "decode_step", "copy_blocks", "swap_out", "swap_in",
-                             "rmsnorm", "silu_mul"],
+                    choices=["attention", "rope_cache", "decode_step", "step", "copy_blocks", "swap_out",
+                             "swap_in", "rmsnorm", "silu_mul"],
                     help="attention (default): the config's decode or prefill line; rope_cache: the fused "
-                         "RoPE + cache write over the config's new tokens; decode_step: RoPE + cache write + "
+                         "RoPE + cache write over the config's new tokens; step: a mixed prefill + decode "
+                         "attention-layer step through the C++ host step layer (rllm_amd/host/step_bench); "
+                         "decode_step: RoPE + cache write + "
                          "decode attention, eager and replayed from a hipGraph; copy_blocks / swap_out / swap_in: "
                          "block-list moves over a 32-layer cache; rmsnorm / silu_mul: at Llama-3-8B widths")
     ap.add_argument("--tp", type=int, default=1,
@@ -537,6 +539,14 @@ def main() -> int:
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
     args = ap.parse_args()
 
+    if args.op == "step":
+        # the C++ program runs as a child process (nothing here has touched the GPU)
+        import subprocess
+        exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "rllm_amd", "host", "_build", "step_bench")
+        if not os.path.exists(exe):
+            print(f"{exe} is not built; run __graft_entry__.build()", file=sys.stderr)
+            return 2
+        return subprocess.run([exe, "--steps", str(args.steps), "--warmup", str(args.warmup)]).returncode
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the decode path "
               "would shard by sequence / kv head with no exchange between GPUs", file=sys.stderr)

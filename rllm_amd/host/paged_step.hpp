@@ -54,6 +54,11 @@ public:
         void* d = nullptr;
         if (hipMalloc(&d, m.capacity_) != hipSuccess) return fail(m);
         m.device_ = static_cast<uint8_t*>(d);
+        // a second stream (default priority) on which paged_attention_step
+        // runs the prefill group beside the decode group
+        if (hipStreamCreateWithFlags(&m.side_, hipStreamNonBlocking) != hipSuccess) return fail(m);
+        if (hipEventCreateWithFlags(&m.fork_, hipEventDisableTiming) != hipSuccess) return fail(m);
+        if (hipEventCreateWithFlags(&m.join_, hipEventDisableTiming) != hipSuccess) return fail(m);
         return Result<DeviceStepMetadata>::ok(std::move(m));
     }
 
@@ -72,6 +77,12 @@ public:
             }
             device_ = o.device_;
             o.device_ = nullptr;
+            side_ = o.side_;
+            fork_ = o.fork_;
+            join_ = o.join_;
+            o.side_ = nullptr;
+            o.fork_ = nullptr;
+            o.join_ = nullptr;
             capacity_ = o.capacity_;
             next_ = o.next_;
             num_tokens = o.num_tokens;
@@ -244,6 +255,14 @@ private:
             copied_[i] = nullptr;
             staging_[i] = nullptr;
         }
+        if (side_) {
+            (void)hipStreamSynchronize(side_);
+            (void)hipStreamDestroy(side_);
+        }
+        if (fork_) (void)hipEventDestroy(fork_);
+        if (join_) (void)hipEventDestroy(join_);
+        side_ = nullptr;
+        fork_ = join_ = nullptr;
         if (device_) (void)hipFree(device_);
         device_ = nullptr;
     }
@@ -253,6 +272,14 @@ private:
     uint8_t* device_ = nullptr;
     size_t capacity_ = 0;
     int next_ = 0;
+    hipStream_t side_ = nullptr;
+    hipEvent_t fork_ = nullptr, join_ = nullptr;
+
+public:
+    // the side stream and the fork / join events of paged_attention_step
+    hipStream_t side_stream() const { return side_; }
+    hipEvent_t fork_event() const { return fork_; }
+    hipEvent_t join_event() const { return join_; }
 };
 
 // Rotary embedding inputs for paged_attention_step (device tables from
@@ -311,12 +338,32 @@ inline Result<void> paged_attention_step(const DeviceStepMetadata& m, void* out,
     const float scale = p.scale;
     const bool fp8 = kv == DType::FP8E4M3 || kv == DType::FP8E5M2;
     const float ks = fp8 ? k_scale : 1.0f, vs = fp8 ? v_scale : 1.0f;
-    // 2. prefill group
+    // 2. prefill group.  With decode work too, it runs on the side stream,
+    // forked after the cache write and joined before the call returns, so a
+    // small prefill chunk (few workgroups) shares the GPU with the decode
+    // group instead of running alone.  The two write disjoint rows of out.
+    const bool fork = m.num_prefill_seqs > 0 && m.num_decode_seqs > 0 && m.side_stream() != nullptr;
     if (m.num_prefill_seqs > 0) {
+        uintptr_t pst = st;
+        if (fork) {
+            if (const hipError_t e = hipEventRecord(m.fork_event(), stream); e != hipSuccess)
+                return check(static_cast<int32_t>(e));
+            if (const hipError_t e = hipStreamWaitEvent(m.side_stream(), m.fork_event(), 0); e != hipSuccess)
+                return check(static_cast<int32_t>(e));
+            pst = reinterpret_cast<uintptr_t>(m.side_stream());
+        }
         const Result<void> r = check(rllm_paged_attention_prefill_ex(
             out, q, key_cache, value_cache, m.prefill_block_tables, m.prefill_seq_lens, m.prefill_query_start_loc,
-            m.num_prefill_seqs, m.num_prefill_tokens, hq, hkv, d, bs, m.prefill_max_blocks, scale, a, c, ks, vs, st));
-        if (r.is_err()) return r;
+            m.num_prefill_seqs, m.num_prefill_tokens, hq, hkv, d, bs, m.prefill_max_blocks, scale, a, c, ks, vs, pst));
+        if (fork) {
+            // recorded even after an error: `stream` joins it below in every case
+            if (const hipError_t e = hipEventRecord(m.join_event(), m.side_stream()); e != hipSuccess)
+                return check(static_cast<int32_t>(e));
+        }
+        if (r.is_err()) {
+            if (fork) (void)hipStreamWaitEvent(stream, m.join_event(), 0);
+            return r;
+        }
     }
     // 3. decode group: its tokens follow the prefill tokens
     if (m.num_decode_seqs > 0) {
@@ -327,6 +374,11 @@ inline Result<void> paged_attention_step(const DeviceStepMetadata& m, void* out,
             static_cast<uint8_t*>(out) + off, static_cast<const uint8_t*>(q) + off, key_cache, value_cache,
             m.decode_block_tables, m.decode_seq_lens, m.num_decode_seqs, hq, hkv, d, bs, m.decode_max_blocks, scale,
             a, c, ks, vs, 0, nullptr, 0, st));
+        // join: later work on `stream` (the next step's metadata upload
+        // included) waits for the prefill group
+        if (fork)
+            if (const hipError_t e = hipStreamWaitEvent(stream, m.join_event(), 0); e != hipSuccess && r.is_ok())
+                return check(static_cast<int32_t>(e));
         if (r.is_err()) return r;
     }
     return Result<void>::ok();
