@@ -22,7 +22,9 @@ FP8 = (O.FP8_E4M3, O.FP8_E5M2)
 # (head_dim, q heads, kv heads, block size, q kind, kv kind)
 SHAPES = [(96, 12, 4, 16, O.BF16, O.BF16), (256, 16, 4, 32, O.BF16, O.BF16), (80, 4, 4, 8, O.F16, O.F16),
           (64, 32, 2, 16, O.BF16, O.BF16), (512, 4, 2, 16, O.BF16, O.FP8_E4M3), (1024, 2, 1, 4, O.F16, O.F16),
-          (128, 12, 4, 1, O.BF16, O.FP8_E5M2), (40, 6, 2, 64, O.BF16, O.BF16)]
+          (128, 12, 4, 1, O.BF16, O.FP8_E5M2), (40, 6, 2, 64, O.BF16, O.BF16),
+          (192, 10, 2, 16, O.F16, O.FP8_E5M2), (96, 24, 8, 32, O.F16, O.FP8_E4M3),
+          (128, 16, 16, 8, O.BF16, O.FP8_E4M3), (64, 7, 7, 8, O.F16, O.F16)]
 
 
 def _kv(k, v, kind, dev):
