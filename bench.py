@@ -534,6 +534,9 @@ def main() -> int:
     ap.add_argument("--kv", default="bf16", choices=["bf16", "fp8_e4m3", "fp8_e5m2"],
                     help="config 5: KV cache dtype of the prefill line (FP8 written by the "
                          "library's cache write, scales amax / max finite)")
+    ap.add_argument("--prefill-seqs", type=int, default=0,
+                    help="config 5: time only the first N sequences' chunks (1: one prompt, the small-batch "
+                         "path that splits the KV range)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
@@ -570,6 +573,11 @@ def main() -> int:
     if args.op in ("rmsnorm", "silu_mul"):
         return bench_fused(args, w, lib, dev)
     if args.config == 5:
+        if 0 < args.prefill_seqs < w.num_seqs:
+            n = args.prefill_seqs
+            w = dataclasses.replace(w, name=f"{w.name}_{n}seq", seq_lens=w.seq_lens[:n].copy(),
+                                    block_tables=np.ascontiguousarray(w.block_tables[:n]),
+                                    query_lens=w.query_lens[:n].copy())
         return bench_prefill(args, w, lib, dev)
     if args.tp > 1:
         if w.num_kv_heads % args.tp:
