@@ -472,34 +472,64 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 }
 
 // Merges the KV splits of every output row (token * Hq + q head): one wave
-// per row, log-sum-exp over the splits' (max, sum) in the exp2 domain.
+// per row, log-sum-exp over the splits' (max, sum) in the exp2 domain.  Lane l
+// owns the D/64 consecutive elements from l * D/64; every split's (max, sum)
+// and values are loaded before any is used (at most 8 splits).
+constexpr int PF_MAX_SPLITS = 8;
+
 template <int QKIND, int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, int64_t rows) {
     using M = Mfma<QKIND>;
-    constexpr int PER_LANE = D / 64;
+    constexpr int PL = D / 64;   // 1 or 2 consecutive elements per lane
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int lane = threadIdx.x & 63;
-    const float* ml = a.part_ml + row * a.splits * 2;
-    const float* po = a.part_o + row * a.splits * D;
-    float mx = -INFINITY;
-    for (int sp = 0; sp < a.splits; ++sp)
-        if (ml[2 * sp + 1] > 0.f) mx = fmaxf(mx, ml[2 * sp]);
-    float L = 0.f, acc[PER_LANE];
+    const int ns = a.splits;
+    const float* ml = a.part_ml + row * ns * 2;
+    const float* po = a.part_o + row * ns * D + lane * PL;
+    float m[PF_MAX_SPLITS], l[PF_MAX_SPLITS], v[PF_MAX_SPLITS][PL];
 #pragma unroll
-    for (int k = 0; k < PER_LANE; ++k) acc[k] = 0.f;
-    for (int sp = 0; sp < a.splits; ++sp) {
-        const float l = ml[2 * sp + 1];
-        if (!(l > 0.f)) continue;
-        const float wgt = exp2f(ml[2 * sp] - mx) * l;
+    for (int sp = 0; sp < PF_MAX_SPLITS; ++sp) {
+        if (sp < ns) {
+            const f32x2 x = *reinterpret_cast<const f32x2*>(ml + 2 * sp);
+            m[sp] = x[0];
+            l[sp] = x[1];
+            if constexpr (PL == 2) {
+                const f32x2 y = *reinterpret_cast<const f32x2*>(po + sp * D);
+                v[sp][0] = y[0];
+                v[sp][1] = y[1];
+            } else {
+                v[sp][0] = po[sp * D];
+            }
+        } else {
+            m[sp] = -INFINITY;
+            l[sp] = 0.f;
+#pragma unroll
+            for (int k = 0; k < PL; ++k) v[sp][k] = 0.f;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < PF_MAX_SPLITS; ++sp)
+        if (l[sp] > 0.f) mx = fmaxf(mx, m[sp]);
+    float L = 0.f, acc[PL];
+#pragma unroll
+    for (int k = 0; k < PL; ++k) acc[k] = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < PF_MAX_SPLITS; ++sp) {
+        if (!(l[sp] > 0.f)) continue;
+        const float wgt = exp2f(m[sp] - mx) * l[sp];
         L += wgt;
 #pragma unroll
-        for (int k = 0; k < PER_LANE; ++k) acc[k] = fmaf(wgt, po[sp * D + lane + 64 * k], acc[k]);
+        for (int k = 0; k < PL; ++k) acc[k] = fmaf(wgt, v[sp][k], acc[k]);
     }
     const float inv = L > 0.f ? a.v_scale / L : 0.f;
-    uint16_t* dst = static_cast<uint16_t*>(a.out) + row * D;
-#pragma unroll
-    for (int k = 0; k < PER_LANE; ++k) dst[lane + 64 * k] = M::bits(acc[k] * inv);
+    uint16_t* dst = static_cast<uint16_t*>(a.out) + row * D + lane * PL;
+    if constexpr (PL == 2)
+        *reinterpret_cast<uint32_t*>(dst) = static_cast<uint32_t>(M::bits(acc[0] * inv)) |
+                                            (static_cast<uint32_t>(M::bits(acc[1] * inv)) << 16);
+    else
+        dst[0] = M::bits(acc[0] * inv);
 }
 
 template <int QKIND, int KVKIND, int D>
@@ -566,7 +596,7 @@ int64_t prefill_splits(int64_t base_wgs, int64_t max_blocks) {
         return 1;
     const int64_t want = 2 * static_cast<int64_t>(cus);
     if (base_wgs >= want) return 1;
-    int64_t sp = std::min<int64_t>(8, (want + base_wgs - 1) / base_wgs);
+    int64_t sp = std::min<int64_t>(PF_MAX_SPLITS, (want + base_wgs - 1) / base_wgs);
     const int64_t tiles = (max_blocks + PF_NBT - 1) / PF_NBT;
     sp = std::min<int64_t>(sp, tiles / 4);
     return sp > 1 ? sp : 1;
