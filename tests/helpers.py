@@ -65,17 +65,37 @@ def dense_prefill_f64(q_f, k_f, v_f, bt, seq_lens, qsl, scale):
     return out
 
 
-def assert_close(got, ref, tol, what=""):
+# Whole-output bounds applied by default on top of the per-element one.  With
+# N(0,1) inputs the outputs shrink roughly as sqrt(e/ctx), so at long contexts
+# the per-element bound alone admits an all-zero or half-size output; the
+# relative L2 error and the projection scale <got,ref>/<ref,ref> do not.
+# FP8 KV cases get the same bounds: the oracle reads the same bytes, so only
+# the kernel's own rounding separates them.
+REL_L2_MAX = 1e-2
+SCALE_TOL = 1e-2
+
+
+def assert_close(got, ref, tol, what="", rel_l2_max=REL_L2_MAX, scale_tol=SCALE_TOL):
+    """Per-element |got-ref| <= atol + rtol|ref|, every value finite, relative
+    L2 error <= rel_l2_max and |<got,ref>/<ref,ref> - 1| <= scale_tol (None
+    disables a whole-output bound).  Returns the relative L2 error."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     atol, rtol = tol
     err = np.abs(got - ref)
     bound = atol + rtol * np.abs(ref)
     bad = err > bound
-    rel_l2 = float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+    ref_sq = float(np.dot(ref.ravel(), ref.ravel()))
+    rel_l2 = float(np.linalg.norm(got - ref) / max(np.sqrt(ref_sq), 1e-30))
+    proj = float(np.dot(got.ravel(), ref.ravel()) / ref_sq) if ref_sq > 0 else 1.0
     msg = (f"{what}: max_abs={err.max():.3e} max_rel={np.max(err / np.maximum(np.abs(ref), 1e-6)):.3e} "
-           f"rel_l2={rel_l2:.3e} violations={int(bad.sum())}/{bad.size}")
-    assert not bad.any() and np.isfinite(got).all(), msg
+           f"rel_l2={rel_l2:.3e} scale={proj:.5f} violations={int(bad.sum())}/{bad.size}")
+    assert np.isfinite(got).all(), msg + " (non-finite output)"
+    assert not bad.any(), msg
+    if rel_l2_max is not None:
+        assert rel_l2 <= rel_l2_max, msg + f" (relative L2 above {rel_l2_max})"
+    if scale_tol is not None and ref_sq > 0:
+        assert abs(proj - 1.0) <= scale_tol, msg + f" (output scale off by more than {scale_tol})"
     return rel_l2
 
 

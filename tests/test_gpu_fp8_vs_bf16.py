@@ -51,7 +51,9 @@ def test_fp8_kv_against_bf16_kv(dev, kv, rounding, bound):
                           fp8_rounding=rounding)
     got = f32(ops.paged_decode(gq, k8, v8, gbt, gsl, scale, kv_dtype=kv, k_scale=ks, v_scale=vs))
     torch.cuda.synchronize()
-    rel_l2 = assert_close(got, ref, TOL_FP8, f"fp8 kv={kv} rounding={rounding} vs bf16 kv")
+    # FP8 against the bf16-KV run: the quantisation error itself, bounded below
+    rel_l2 = assert_close(got, ref, TOL_FP8, f"fp8 kv={kv} rounding={rounding} vs bf16 kv",
+                          rel_l2_max=None, scale_tol=None)
     print(f"kv={kv} rounding={rounding}: rel_l2 {rel_l2:.4f} (bound {bound})")
     assert rel_l2 <= bound
     if rounding == rllm_amd.FP8_ROUND_NEAREST_EVEN:   # no systematic shrink
