@@ -200,3 +200,26 @@ def host_tensors(w: Workload, seed_offset: int = 0):
     k = normal_bf16_bits(rng, shape)
     v = normal_bf16_bits(rng, shape)
     return q, k, v
+
+
+def device_tensors(w: Workload, device, seed_offset: int = 0):
+    """Seeded N(0, 1) values drawn on the GPU (torch's Philox generator) and
+    rounded to bf16: (q, k, v) device tensors [T,Hq,D] and [nb,Hkv,D,bs].
+    Much faster than host_tensors for the multi-GB configurations; the values
+    differ from host_tensors' (another generator), the distribution does not."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed((SEED_BASE ^ w.index) + 7919 * (seed_offset + 1))
+
+    def draw(shape):
+        out = torch.empty(shape, dtype=torch.bfloat16, device=device)
+        flat = out.view(-1)
+        step = 1 << 26   # bounded float32 temporaries
+        for i in range(0, flat.numel(), step):
+            n = min(step, flat.numel() - i)
+            flat[i:i + n] = torch.randn(n, generator=g, device=device, dtype=torch.float32)
+        return out
+
+    q = draw((w.num_tokens, w.num_q_heads, w.head_dim))
+    shape = (w.num_blocks, w.num_kv_heads, w.head_dim, w.block_size)
+    return q, draw(shape), draw(shape)
