@@ -38,6 +38,7 @@
 // the kernel is bound by HBM bandwidth.
 #include "common.h"
 #include "generic_attention.h"
+#include "workspace.h"
 #include "../../include/rllm_kernels.h"
 
 #include <algorithm>
@@ -1109,36 +1110,6 @@ bool make_partition_plan(int64_t num_seqs, int64_t num_q_heads, int64_t head_dim
     return true;
 }
 
-// Library-owned split-K scratch, one buffer per (device, stream, mode) so calls
-// on different streams never share memory and partitioned partials never land
-// on the stream kernel's arrival counters.  Grown on demand, kept until exit;
-// zero-filled when allocated (the counters start at zero and every stream call
-// leaves them at zero).
-std::mutex g_ws_mutex;
-std::map<std::tuple<int, uintptr_t, int>, std::pair<void*, int64_t>> g_ws;
-
-int32_t get_workspace(uintptr_t stream, Mode mode, int64_t bytes, void** out) {
-    int dev = 0;
-    RLLM_TRY(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_ws_mutex);
-    auto& e = g_ws[{dev, stream, static_cast<int>(mode)}];
-    if (e.second < bytes) {
-        if (e.first) {
-            // the old buffer may still be read by queued work on this stream
-            RLLM_TRY(hipStreamSynchronize(as_stream(stream)));
-            RLLM_TRY(hipFree(e.first));
-            e.first = nullptr;
-            e.second = 0;
-        }
-        const int64_t rounded = (bytes + (1 << 20) - 1) & ~int64_t((1 << 20) - 1);
-        RLLM_TRY(hipMalloc(&e.first, static_cast<size_t>(rounded)));
-        e.second = rounded;
-        RLLM_TRY(hipMemset(e.first, 0, static_cast<size_t>(rounded)));
-    }
-    *out = e.first;
-    return 0;
-}
-
 // the kernels of one (q type, kv type, head_dim, group size) instantiation
 struct Kernels {
     const void* part;
@@ -1242,21 +1213,32 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
     a.num_q_heads = static_cast<int32_t>(hq);
     a.num_kv_heads = static_cast<int32_t>(hkv);
     a.max_blocks = static_cast<int32_t>(maxb);
-    a.part_chunks = plan.part_chunks;
-    a.max_parts = plan.max_parts;
-    a.num_waves = plan.num_waves;
     const bool fp8 = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
     a.s_scale = scale * LOG2E * (fp8 ? k_scale : 1.0f);
     a.v_scale = fp8 ? v_scale : 1.0f;
 
+    void* ws = workspace;
     if (plan.ws_bytes > 0) {
-        void* ws = workspace;
         if (ws) {
             RLLM_CHECK_ARG(workspace_bytes >= plan.ws_bytes);
         } else {
-            int32_t rc = get_workspace(stream, plan.mode, plan.ws_bytes, &ws);
+            // library-owned scratch; the stream kernel's arrival counters must
+            // start at zero (every call leaves them at zero)
+            const int role = plan.mode == Mode::Stream ? WS_DECODE_STREAM : WS_DECODE_PARTS;
+            int32_t rc = g_workspaces.get(stream, role, plan.ws_bytes, plan.mode == Mode::Stream, &ws);
             if (rc) return rc;
+            if (!ws) {
+                // capturing on a stream whose scratch is missing or too small:
+                // one wave per (sequence, kv head), which needs none
+                RLLM_CHECK_ARG(make_partition_plan(num_seqs, hq, d, maxb, -1, &plan));
+                RLLM_CHECK_ARG(num_seqs * hkv <= INT32_MAX);
+            }
         }
+    }
+    a.part_chunks = plan.part_chunks;
+    a.max_parts = plan.max_parts;
+    a.num_waves = plan.num_waves;
+    if (plan.ws_bytes > 0) {
         if (plan.mode == Mode::Stream) {
             a.arrivals = static_cast<uint32_t*>(ws);
             a.part_out = reinterpret_cast<float*>(static_cast<char*>(ws) + stream_counter_bytes(plan.max_waves));

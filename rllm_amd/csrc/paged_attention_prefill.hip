@@ -38,6 +38,7 @@
 //               tiles of one kv head share one XCD's L2.
 #include "common.h"
 #include "generic_attention.h"
+#include "workspace.h"
 #include "../../include/rllm_kernels.h"
 
 #include <algorithm>
@@ -482,7 +483,9 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, int64
     using M = Mfma<QKIND>;
     constexpr int PL = D / 64;   // 1 or 2 consecutive elements per lane
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    // rows past the last sequence's chunk have no partials: left untouched,
+    // as the unsplit kernel leaves them
+    if (row >= rows || row >= static_cast<int64_t>(a.query_start_loc[a.num_seqs]) * a.num_q_heads) return;
     const int lane = threadIdx.x & 63;
     const int ns = a.splits;
     const float* ml = a.part_ml + row * ns * 2;
@@ -551,41 +554,6 @@ int32_t launch_prefill_d(int64_t D, int64_t G, const PrefillArgs& a, dim3 grid, 
     return (int32_t)hipErrorInvalidValue;
 }
 
-// KV-split workspace per (device, stream), grown on demand: the partials of
-// one call are read by its merge kernel on the same stream.
-std::mutex g_pf_ws_mutex;
-std::map<std::pair<int, uintptr_t>, std::pair<void*, int64_t>> g_pf_ws;
-
-// *out = nullptr (and 0 returned) when the buffer would have to grow while the
-// stream is being captured: allocation is not allowed there, and the caller
-// then runs unsplit.
-int32_t split_workspace(uintptr_t stream, int64_t bytes, void** out) {
-    int dev = 0;
-    RLLM_TRY(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_pf_ws_mutex);
-    auto& e = g_pf_ws[{dev, stream}];
-    if (e.second < bytes) {
-        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-        RLLM_TRY(hipStreamIsCapturing(as_stream(stream), &cap));
-        if (cap != hipStreamCaptureStatusNone) {
-            *out = nullptr;
-            return 0;
-        }
-        if (e.first) {
-            // queued work on this stream may still read the old buffer
-            RLLM_TRY(hipStreamSynchronize(as_stream(stream)));
-            RLLM_TRY(hipFree(e.first));
-            e.first = nullptr;
-            e.second = 0;
-        }
-        const int64_t rounded = (bytes + (1 << 20) - 1) & ~int64_t((1 << 20) - 1);
-        RLLM_TRY(hipMalloc(&e.first, static_cast<size_t>(rounded)));
-        e.second = rounded;
-    }
-    *out = e.first;
-    return 0;
-}
-
 // KV splits for a launch of base_wgs workgroups over tables max_blocks wide:
 // enough to give the device two workgroups per CU, at most 8, and only while
 // each split keeps at least 4 of the widest row's 64-token tiles.
@@ -652,7 +620,9 @@ int32_t prefill_impl(void* out, const void* q, const void* kc, const void* vc, c
     if (splits > 1) {
         RLLM_CHECK_ARG(nwg * splits <= INT32_MAX && rows <= (int64_t(1) << 40) / (splits * (d + 2)));
         void* ws = nullptr;
-        const int32_t wrc = split_workspace(stream, rows * splits * (d + 2) * 4, &ws);
+        // nullptr while capturing on a stream whose scratch is missing or too
+        // small: the call then runs unsplit
+        const int32_t wrc = g_workspaces.get(stream, WS_PREFILL_SPLITS, rows * splits * (d + 2) * 4, false, &ws);
         if (wrc) return wrc;
         if (ws) {
             a.part_o = static_cast<float*>(ws);

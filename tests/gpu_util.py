@@ -31,3 +31,24 @@ def ptr(t) -> int:
 def log_case(msg: str) -> None:
     """Name the case before a GPU step (a fault can end the process)."""
     print(f"[case] {msg}", flush=True)
+
+
+class RawStream:
+    """A HIP stream the library has never seen (torch.cuda.Stream() draws from a
+    reused pool): created with hipStreamCreate (default priority), wrapped as a
+    torch ExternalStream, destroyed on exit after a device synchronisation."""
+
+    def __enter__(self):
+        import ctypes
+        self._hip = ctypes.CDLL("libamdhip64.so")
+        h = ctypes.c_void_p()
+        rc = self._hip.hipStreamCreate(ctypes.byref(h))
+        assert rc == 0, f"hipStreamCreate: {rc}"
+        self.handle = h
+        self.stream = torch.cuda.ExternalStream(h.value)
+        return self.stream
+
+    def __exit__(self, *exc):
+        torch.cuda.synchronize()
+        self._hip.hipStreamDestroy(self.handle)
+        return False

@@ -15,8 +15,8 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import log_case, t16, ti
-from helpers import random_case
+from gpu_util import RawStream, f32, log_case, t16, ti
+from helpers import TOL_BF16, assert_close, random_case
 from rllm_amd import attention as A
 from rllm_amd import ops
 
@@ -110,6 +110,10 @@ def test_prefill_graph_replays_match_eager(dev):
     log_case("graph prefill eager")
     eager = ops.paged_prefill(q, kc, vc, btd, sld, qsld, scale)
     torch.cuda.synchronize()
+    ref = O.paged_attention_prefill(O.encode(f32(q), O.BF16), O.BF16, O.encode(f32(kc), O.BF16),
+                                    O.encode(f32(vc), O.BF16), O.BF16, bt, ctx.astype(np.int32), qsl,
+                                    scale, precision=1)
+    assert_close(f32(eager), ref, TOL_BF16, "prefill eager vs oracle")
     static_out = torch.zeros_like(q)
     g = torch.cuda.CUDAGraph()
     # a small batch splits every row's KV range; the split workspace is held
@@ -129,6 +133,7 @@ def test_prefill_graph_replays_match_eager(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(static_out, eager), f"replay {r} differs from the eager call"
+        assert_close(f32(static_out), ref, TOL_BF16, f"prefill replay {r} vs oracle")
     # captured on a stream that has no split workspace: the call runs unsplit
     # (no allocation inside the capture) and still matches within tolerance
     g2 = torch.cuda.CUDAGraph()
@@ -137,8 +142,7 @@ def test_prefill_graph_replays_match_eager(dev):
         ops.paged_prefill(q, kc, vc, btd, sld, qsld, scale, out=out2, validate=False)
     g2.replay()
     torch.cuda.synchronize()
-    diff = (out2.float() - eager.float()).abs()
-    assert bool((diff <= 2e-2 + 1e-2 * eager.float().abs()).all())
+    assert_close(f32(out2), ref, TOL_BF16, "prefill captured unsplit vs oracle")
 
 
 def test_full_decode_step_graph_with_rope_and_fused_ops(dev):
@@ -206,3 +210,104 @@ def test_full_decode_step_graph_with_rope_and_fused_ops(dev):
         step(o_out, o_q, o_n, o_a)            # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(o_out, e_out)
+
+
+def _decode_case(dev, seed, B, ctx_range):
+    rng = np.random.default_rng(seed)
+    q, k, v, bt, sl = random_case(rng, B, 32, 8, 128, ctx_range)
+    qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
+    scale = 1 / np.sqrt(128)
+    ref = O.paged_attention_decode(qb, O.BF16, kb, vb, O.BF16, bt, sl, scale, precision=1)
+    bf = torch.bfloat16
+    return dict(q=t16(qb, bf, dev), kc=t16(kb, bf, dev), vc=t16(vb, bf, dev), bt=ti(bt, torch.int32, dev),
+                sl=ti(sl, torch.int32, dev), scale=scale, ref=ref)
+
+
+def test_decode_graph_without_workspace_vs_oracle(dev):
+    """Decode captured with no caller workspace, through the reference-signature
+    path (library-owned scratch).  On a fresh stream the library holds no
+    scratch and may not allocate inside the capture: the captured call runs one
+    wave per (sequence, kv head).  After one eager call the stream holds
+    scratch and a second capture uses the stream split.  Every replay is
+    compared with the oracle."""
+    x = _decode_case(dev, 131, 12, (100, 3000))
+
+    def call(out):
+        ops.paged_decode(x["q"], x["kc"], x["vc"], x["bt"], x["sl"], x["scale"], out=out, validate=False)
+
+    with RawStream() as fresh:
+        _capture_without_then_with_scratch(x, call, fresh)
+
+
+def _capture_without_then_with_scratch(x, call, fresh):
+    out1 = torch.zeros_like(x["q"])
+    g1 = torch.cuda.CUDAGraph()
+    log_case("graph decode capture on a fresh stream, no workspace")
+    with torch.cuda.graph(g1, stream=fresh):
+        call(out1)
+    torch.cuda.synchronize()
+    # eager on the same stream: allocates the stream's scratch
+    with torch.cuda.stream(fresh):
+        eager = torch.zeros_like(x["q"])
+        call(eager)
+    torch.cuda.synchronize()
+    assert_close(f32(eager), x["ref"], TOL_BF16, "eager vs oracle")
+    out2 = torch.zeros_like(x["q"])
+    g2 = torch.cuda.CUDAGraph()
+    log_case("graph decode capture with the stream's scratch")
+    with torch.cuda.graph(g2, stream=fresh):
+        call(out2)
+    torch.cuda.synchronize()
+    for r in range(3):
+        out1.zero_()
+        out2.zero_()
+        log_case(f"graph decode replays {r} (single pass, stream split)")
+        g1.replay()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert_close(f32(out1), x["ref"], TOL_BF16, f"replay {r} of the capture without scratch")
+        assert_close(f32(out2), x["ref"], TOL_BF16, f"replay {r} of the capture with scratch")
+        assert torch.equal(out2, eager)
+
+
+def test_decode_graph_survives_scratch_growth(dev):
+    """A graph captured with the stream's library-owned scratch keeps that
+    buffer's address.  A later eager call on the same stream that needs more
+    scratch must not free it: the library retires the old buffer and allocates
+    a larger one.  The graph is then replayed and compared with the oracle."""
+    small = _decode_case(dev, 211, 4, (200, 1200))
+    big = _decode_case(dev, 212, 64, (1000, 4000))
+    with RawStream() as st:
+        _replay_after_growth(small, big, st)
+
+
+def _replay_after_growth(small, big, st):
+    def call(x, out):
+        ops.paged_decode(x["q"], x["kc"], x["vc"], x["bt"], x["sl"], x["scale"], out=out, validate=False)
+
+    with torch.cuda.stream(st):
+        warm = torch.zeros_like(small["q"])
+        call(small, warm)   # the stream's scratch, sized for the small batch
+    torch.cuda.synchronize()
+    out_small = torch.zeros_like(small["q"])
+    g = torch.cuda.CUDAGraph()
+    log_case("graph decode capture (small batch), then scratch growth")
+    with torch.cuda.graph(g, stream=st):
+        call(small, out_small)
+    torch.cuda.synchronize()
+    out_big = torch.zeros_like(big["q"])
+    with torch.cuda.stream(st):
+        call(big, out_big)   # needs more scratch than the captured call's buffer
+    torch.cuda.synchronize()
+    assert_close(f32(out_big), big["ref"], TOL_BF16, "larger eager call vs oracle")
+    for r in range(3):
+        out_small.zero_()
+        log_case(f"graph decode replay {r} after growth")
+        with torch.cuda.stream(st):
+            g.replay()
+        torch.cuda.synchronize()
+        assert_close(f32(out_small), small["ref"], TOL_BF16, f"replay {r} after scratch growth")
+        with torch.cuda.stream(st):
+            call(big, out_big)   # eager work between replays, on the grown buffer
+        torch.cuda.synchronize()
+        assert_close(f32(out_big), big["ref"], TOL_BF16, f"eager call {r} after replay")

@@ -222,3 +222,58 @@ def test_prefill_fp8_every_byte_converts_exactly(dev, fp8, q_kind):
     got = run_prefill(dev, qb, q_kind, kb, vb, fp8, bt, sl, qsl, 0.1)
     want = O.decode(bytes_, fp8).reshape(B, D)
     assert np.array_equal(got[:, 0, :], want)
+
+
+@pytest.mark.parametrize("shape", [(1, 512, 2048), (4, 256, 4096)])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("kv", [O.BF16, O.FP8_E4M3, O.FP8_E5M2])
+def test_prefill_kv_split_vs_oracle(dev, shape, D, kv):
+    """Small batches split every row's KV range over several workgroups and
+    merge the partials (log-sum-exp) in a second kernel: 1 x 512 new tokens on
+    2048 cached and 4 x 256 on 4096 both take that path.  A merge that drops or
+    mis-weights a split fails the relative-L2 and output-scale bounds."""
+    nseq, n_new, cached = shape
+    rng = np.random.default_rng(1000 + nseq + D + 7 * kv)
+    hkv, G = 8, 4
+    q, k, v, bt, sl, qsl = make_case(rng, [n_new] * nseq, [cached] * nseq, hkv * G, hkv, D)
+    qb = O.encode(q, O.BF16)
+    ks = vs = 1.0
+    if kv == O.BF16:
+        kb, vb = O.encode(k, O.BF16), O.encode(v, O.BF16)
+    else:
+        top = 448.0 if kv == O.FP8_E4M3 else 57344.0
+        ks, vs = float(np.abs(k).max() / top), float(np.abs(v).max() / top)
+        kb = O.encode((k / np.float32(ks)).astype(np.float32), kv)
+        vb = O.encode((v / np.float32(vs)).astype(np.float32), kv)
+    scale = 1 / np.sqrt(D)
+    ref = O.paged_attention_prefill(qb, O.BF16, kb, vb, kv, bt, sl, qsl, scale, ks, vs, precision=1)
+    got = run_prefill(dev, qb, O.BF16, kb, vb, kv, bt, sl, qsl, scale, ks, vs,
+                      label=f"kv split {nseq}x{n_new} on {cached} D={D}")
+    assert_close(got, ref, TOL_FP8 if kv != O.BF16 else TOL_BF16, f"kv split {shape} D={D} kv={kv}")
+
+
+def test_prefill_split_leaves_rows_past_the_batch_untouched(dev):
+    """num_tokens larger than query_start_loc[num_seqs]: the rows past the last
+    chunk belong to no sequence.  The split path's merge kernel leaves them as
+    they were, as the unsplit kernel does (1 x 512 on 2048 cached splits)."""
+    rng = np.random.default_rng(77)
+    hq, hkv, D = 32, 8, 128
+    q, k, v, bt, sl, qsl = make_case(rng, [512], [2048], hq, hkv, D)
+    extra = 40
+    T = int(qsl[-1])
+    qb = O.encode(np.concatenate([q, rng.standard_normal((extra, hq, D)).astype(np.float32)]), O.BF16)
+    kb, vb = O.encode(k, O.BF16), O.encode(v, O.BF16)
+    scale = 1 / np.sqrt(D)
+    ref = O.paged_attention_prefill(qb[:T], O.BF16, kb, vb, O.BF16, bt, sl, qsl, scale, precision=1)
+    bf = torch.bfloat16
+    dq, dk, dv = t16(qb, bf, dev), t16(kb, bf, dev), t16(vb, bf, dev)
+    out = torch.full_like(dq, 7.0)
+    dbt, dsl, dqsl = ti(bt, torch.int32, dev), ti(sl, torch.int32, dev), ti(qsl, torch.int32, dev)
+    log_case(f"prefill rows past the batch: num_tokens={T + extra} qsl[-1]={T}")
+    A.paged_attention_prefill_bf16(ptr(out), ptr(dq), ptr(dk), ptr(dv), ptr(dbt), ptr(dsl), ptr(dqsl), 1,
+                                   T + extra, hq, hkv, D, 16, bt.shape[1], scale,
+                                   torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = f32(out)
+    assert np.all(got[T:] == 7.0), "rows past query_start_loc[num_seqs] were written"
+    assert_close(got[:T], ref, TOL_BF16, "rows of the batch")
