@@ -158,6 +158,29 @@ int64_t rllm_paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num
                                                    int64_t max_num_blocks_per_seq,
                                                    int64_t partition_size);
 
+/* New, no counterpart in the reference: rllm_paged_attention_decode_ex with
+ * no workspace argument, for callers that cannot allocate device memory (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It calls no hipMalloc, hipFree or allocating library routine:
+ * its scratch is one fixed device array of RLLM_DECODE_NOALLOC_SCRATCH_BYTES
+ * per GPU, held from library load until the process ends.  A call that would
+ * need more scratch than that (rllm_paged_attention_decode_workspace_size
+ * gives the figure) returns hipErrorOutOfMemory (2) before any launch; the
+ * stream mode of every tuned shape fits.  All calls on one GPU share the
+ * array, whatever their stream: calls that overlap in time on one GPU race
+ * and must be serialised by the caller.  The first call on a device clears
+ * the array's arrival counters with a kernel on `stream`. */
+#define RLLM_DECODE_NOALLOC_SCRATCH_BYTES (24ll << 20)
+int32_t rllm_paged_attention_decode_noalloc(void *output, const void *query,
+                                            const void *key_cache, const void *value_cache,
+                                            const int32_t *block_tables, const int32_t *seq_lens,
+                                            int64_t num_seqs, int64_t num_q_heads,
+                                            int64_t num_kv_heads, int64_t head_dim,
+                                            int64_t block_size, int64_t max_num_blocks_per_seq,
+                                            float scale, int32_t q_dtype, int32_t kv_dtype,
+                                            float k_scale, float v_scale, int64_t partition_size,
+                                            uintptr_t stream);
+
 /* ======================================================================
  * Prefill / chunked-prefill paged attention (MFMA)
  * ==================================================================== */
