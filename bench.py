@@ -36,21 +36,45 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_stream_bf16_config2_traffic.md")
+PROFILES = os.path.join(ROOT, "profiles")
+# the sources whose kernels a traffic summary measured: a summary counts only
+# while their digest matches the one recorded with it
+KERNEL_SOURCES = {
+    "decode": ["rllm_amd/csrc/paged_attention_decode.hip", "rllm_amd/csrc/common.h"],
+    "prefill": ["rllm_amd/csrc/paged_attention_prefill.hip", "rllm_amd/csrc/common.h"],
+}
 
 
-def measured_traffic(workload: str):
-    """HBM bytes per decode launch from the committed counter summary: the
-    line `traffic_bytes_per_launch: N (workload W)`; None when absent."""
-    try:
-        with open(TRAFFIC_SUMMARY) as f:
-            for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+def source_digest(kind: str) -> str:
+    """sha256 (first 16 hex digits) over the kernel sources of `kind`."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES[kind]:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(workload: str, kind: str = "decode"):
+    """HBM bytes per launch from the committed counter summaries
+    (profiles/*_traffic.md): the line `traffic_bytes_per_launch: N (workload W)
+    source_digest: H`.  None when no summary covers the workload or when the
+    kernel sources changed since it was recorded (H differs)."""
+    import glob
+    want = source_digest(kind)
+    for path in sorted(glob.glob(os.path.join(PROFILES, "*_traffic.md"))):
+        try:
+            with open(path) as f:
+                for line in f:
+                    if not line.startswith("traffic_bytes_per_launch:"):
+                        continue
                     parts = line.split()
-                    if f"{workload})" in line:
-                        return int(parts[1])
-    except OSError:
-        pass
+                    if f"{workload})" not in line:
+                        continue
+                    dig = parts[parts.index("source_digest:") + 1] if "source_digest:" in parts else None
+                    return int(parts[1]) if dig == want else None
+        except OSError:
+            continue
     return None
 
 
@@ -84,6 +108,22 @@ def cpu_baseline(w, qb, kb, vb, reps: int = 5):
             "ms_per_call": round(med * 1e3, 3),
             "sample": f"full config-{w.index} batch ({w.num_seqs} seqs, sum ctx "
                       f"{int(w.seq_lens.sum())}), fp32, median of {len(times)} runs after 1 warm-up"}
+
+
+def calibrate_copy(args, dev, sh):
+    """--calibrate-copy-mib N: the library's block copy over exactly N MiB,
+    three times, so a counter run can scale FETCH_SIZE / WRITE_SIZE."""
+    if args.calibrate_copy_mib <= 0:
+        return
+    import torch
+    from rllm_amd import cache_ops
+    n = args.calibrate_copy_mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        cache_ops.cache_block_copy(src.data_ptr(), dst.data_ptr(), n, 1, sh)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def per_launch_ms(step, n, stream):
@@ -178,13 +218,48 @@ def bench_prefill(args, w, lib, dev) -> int:
                    "head_dim": w.head_dim, "block_size": w.block_size,
                    "context_per_seq": int(w.seq_lens.max()), "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(w.name if args.kv == "bf16" else f"{w.name}_{args.kv}kv", "prefill"),
                      "kernel_ms": round(kernel_ms, 5),
                      "per_launch_ms_p10_p50_p90": [round(float(np.percentile(call_ms, q)), 5) for q in (10, 50, 90)],
                      "algorithmic_flops": int(flops)},
     }
+    calibrate_copy(args, dev, sh)
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline_prefill(w, qb, kb, vb)
     print(json.dumps(res), flush=True)
     return 0
+
+
+def cpu_baseline_prefill(w, qb, kb, vb):
+    """The oracle's fp32 chunked prefill (the reference CPU attention with the
+    context-offset causal mask) on all usable host cores, over a bounded sample
+    of the batch: the first sequences whose chunks total at least 1/8 of the
+    FLOPs (one of config 5's eight), timed as often as fits in ~10 s."""
+    import numpy as np
+    import oracle as O
+    cores = _cores()
+    n = 1
+    sub = dataclasses.replace(w, seq_lens=w.seq_lens[:n].copy(), query_lens=w.query_lens[:n].copy(),
+                              block_tables=np.ascontiguousarray(w.block_tables[:n]))
+    T = sub.num_tokens
+    qsl = sub.query_start_loc()
+    args = (qb[:T], O.BF16, kb, vb, O.BF16, sub.block_tables, sub.seq_lens, qsl, w.scale)
+    O.paged_attention_prefill(*args, precision=0, nthreads=cores)   # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        O.paged_attention_prefill(*args, precision=0, nthreads=cores)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 10.0 or len(times) >= 5:
+            break
+    med = float(np.median(times))
+    flops = sub.prefill_flops()
+    return {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "ms_per_call": round(med * 1e3, 2),
+            "sample": f"{n} of {w.num_seqs} sequences ({T} new tokens on {int(sub.seq_lens[0]) - T} cached, "
+                      f"{flops / 1e9:.2f} GFLOP), fp32, median of {len(times)} runs after 1 warm-up"}
 
 
 def bench_rope_cache(args, w, lib, dev) -> int:
@@ -258,6 +333,117 @@ def bench_rope_cache(args, w, lib, dev) -> int:
                      "per_launch_ms_p10_p50_p90": [round(float(np.percentile(call_ms, q)), 5) for q in (10, 50, 90)],
                      "algorithmic_bytes": nbytes},
     }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def cache_write_bytes(n, hkv, d, e_in, e_cache):
+    """Algorithmic bytes of one reshape_and_cache call: read k and v, write
+    both cache entries, read the slots (8 B each)."""
+    return n * hkv * d * 2 * (e_in + e_cache) + n * 8
+
+
+def bench_cache_write(args, w, lib, dev) -> int:
+    """--op cache_write: reshape_and_cache of one new token per sequence (the
+    decode step's write) into random distinct slots of the pool's free
+    blocks.  Config 3: 256 tokens into the FP8 E4M3 pool with per-tensor scales
+    amax / 448 (never powers of two, so every value is divided correctly
+    rounded).  Also times the oracle's cache write on the same inputs."""
+    import numpy as np
+    import torch
+
+    import rllm_amd
+    from rllm_amd import ops
+    n, hkv, D, bs, nb = w.num_seqs, w.num_kv_heads, w.head_dim, w.block_size, w.num_blocks
+    fp8 = w.kv_dtype.startswith("fp8")
+    kv = (rllm_amd.DTYPE_FP8_E4M3 if w.kv_dtype == "fp8_e4m3" else rllm_amd.DTYPE_FP8_E5M2) if fp8 \
+        else rllm_amd.DTYPE_BF16
+    rng = np.random.default_rng(0x524C4C4D ^ w.index ^ 0xF8)
+    free = np.setdiff1d(np.arange(nb), w.block_tables.ravel())
+    pick = rng.choice(free.size * bs, size=n, replace=False)
+    slots_h = (free[pick // bs].astype(np.int64) * bs + pick % bs).astype(np.int64)
+    slots = torch.from_numpy(slots_h).to(dev)
+    g = torch.Generator(device="cpu").manual_seed(w.index)
+    sets = [(torch.randn(n, hkv, D, generator=g).to(torch.bfloat16).to(dev),
+             torch.randn(n, hkv, D, generator=g).to(torch.bfloat16).to(dev)) for _ in range(4)]
+    kc = torch.zeros((nb, hkv, D, bs), dtype=torch.uint8 if fp8 else torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    # per-tensor scales as a pool of N(0,1) values would give them (amax / max finite)
+    top = 448.0 if kv == rllm_amd.DTYPE_FP8_E4M3 else 57344.0
+    ks = float(max(float(k.float().abs().max()) for k, _ in sets)) / top if fp8 else 1.0
+    vs = float(max(float(v.float().abs().max()) for _, v in sets)) / top if fp8 else 1.0
+    stream = torch.cuda.current_stream()
+    sh = int(stream.cuda_stream)
+    if fp8:
+        fn = lib.rllm_cache_write_fp8_ex
+        ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in sets]
+
+        def step(i):
+            kp, vp = ptrs[i & 3]
+            rc = fn(kc.data_ptr(), vc.data_ptr(), kp, vp, slots.data_ptr(), n, hkv, D, bs, nb,
+                    rllm_amd.DTYPE_BF16, ks, vs, kv, rllm_amd.FP8_ROUND_TOWARD_ZERO, sh)
+            if rc:
+                raise rllm_amd.KernelError(rc, "rllm_cache_write_fp8_ex")
+    else:
+        fn = lib.rllm_cache_write_bf16
+        ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in sets]
+
+        def step(i):
+            kp, vp = ptrs[i & 3]
+            rc = fn(kc.data_ptr(), vc.data_ptr(), kp, vp, slots.data_ptr(), n, hkv, D, bs, nb, sh)
+            if rc:
+                raise rllm_amd.KernelError(rc, "rllm_cache_write_bf16")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    region_ms = ev0.elapsed_time(ev1)
+    call_ms = per_launch_ms(step, args.steps, stream)
+    nbytes = cache_write_bytes(n, hkv, D, 2, 1 if fp8 else 2)
+    ms_per_step = wall * 1e3 / args.steps
+    kernel_ms = region_ms / args.steps
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    res = {
+        "metric": "reshape_and_cache GB/s (algorithmic bytes) + us per call",
+        "value": round(nbytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": w.kv_dtype, "data": "synthetic N(0,1) (seeded), random free slots",
+        "config": {"workload": w.name, "config_index": w.index, "op": "cache_write", "num_tokens": n,
+                   "num_kv_heads": hkv, "head_dim": D, "block_size": bs, "kv_dtype": w.kv_dtype,
+                   "k_scale": ks, "v_scale": vs, "parallelism": "single GPU"},
+        "us_per_call": round(kernel_ms * 1e3, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_ms": round(kernel_ms, 5),
+                     "per_launch_ms_p10_p50_p90": [round(float(np.percentile(call_ms, q)), 5) for q in (10, 50, 90)],
+                     "algorithmic_bytes": nbytes},
+    }
+    if not args.no_cpu_baseline:
+        import oracle as O
+        kb = O.encode(sets[0][0].float().cpu().numpy(), O.BF16)
+        vb = O.encode(sets[0][1].float().cpu().numpy(), O.BF16)
+        hk = np.zeros((nb, hkv, D, bs), np.uint8 if fp8 else np.uint16)
+        hv = np.zeros_like(hk)
+        okind = (O.FP8_E4M3 if kv == rllm_amd.DTYPE_FP8_E4M3 else O.FP8_E5M2) if fp8 else O.BF16
+        times = []
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < 10.0 and len(times) < 2000:
+            t1 = time.perf_counter()
+            O.cache_write(hk, hv, kb, vb, slots_h, bs, O.BF16, okind, ks, vs)
+            times.append(time.perf_counter() - t1)
+        med = float(np.median(times))
+        res["cpu_baseline"] = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                               "us_per_call": round(med * 1e6, 2),
+                               "sample": f"the same {n}-token write, median of {len(times)} calls"}
     print(json.dumps(res), flush=True)
     return 0
 
@@ -520,10 +706,11 @@ def main() -> int:
                     help="benchmark config: 2 (default) is the headline decode line; 5 is chunked prefill")
     ap.add_argument("--partition", type=int, default=0, help="0 auto, <0 single pass, >0 tokens")
     ap.add_argument("--op", default="attention",
-                    choices=["attention", "rope_cache", "decode_step", "step", "copy_blocks", "swap_out",
-                             "swap_in", "rmsnorm", "silu_mul"],
+                    choices=["attention", "rope_cache", "cache_write", "decode_step", "step", "copy_blocks",
+                             "swap_out", "swap_in", "rmsnorm", "silu_mul"],
                     help="attention (default): the config's decode or prefill line; rope_cache: the fused "
-                         "RoPE + cache write over the config's new tokens; step: a mixed prefill + decode "
+                         "RoPE + cache write over the config's new tokens; cache_write: reshape_and_cache of "
+                         "one new token per sequence into free slots; step: a mixed prefill + decode "
                          "attention-layer step through the C++ host step layer (rllm_amd/host/step_bench); "
                          "decode_step: RoPE + cache write + "
                          "decode attention, eager and replayed from a hipGraph; copy_blocks / swap_out / swap_in: "
@@ -566,6 +753,8 @@ def main() -> int:
     w = workloads.config(args.config)
     if args.op == "rope_cache":
         return bench_rope_cache(args, w, lib, dev)
+    if args.op == "cache_write":
+        return bench_cache_write(args, w, lib, dev)
     if args.op == "decode_step":
         return bench_decode_step(args, w, lib, dev)
     if args.op in ("copy_blocks", "swap_out", "swap_in"):
@@ -695,15 +884,7 @@ def main() -> int:
     }
     if w.index == 4:
         res["roofline"]["logical_bytes"] = w.decode_bytes()
-    if args.calibrate_copy_mib > 0:
-        from rllm_amd import cache_ops
-        n = args.calibrate_copy_mib << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            cache_ops.cache_block_copy(src.data_ptr(), dst.data_ptr(), n, 1, sh)
-        torch.cuda.synchronize()
-        del src, dst
+    calibrate_copy(args, dev, sh)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, qb, kb, vb)
     print(json.dumps(res), flush=True)
