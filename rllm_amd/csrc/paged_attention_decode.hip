@@ -59,6 +59,19 @@ constexpr int SC_TOKENS = SC_BLOCKS * BS;    // 512
 #ifndef RLLM_PF_V
 #define RLLM_PF_V 4
 #endif
+// Virtual work items at the start of every (sequence, kv head) row in the
+// stream-mode work list of a batch with mixed lengths, in 16-bit cache blocks
+// (twice as many FP8 blocks): a row's start-up (block table, q, the first
+// loads of its window pipeline) costs a wave about this much streaming time,
+// so shares that start more rows get fewer blocks (config 2: 4 blocks, 117 ->
+// 112 us with the progress priority below).
+#ifndef RLLM_ROW_COST
+#define RLLM_ROW_COST 4
+#endif
+#ifndef RLLM_STREAM_PRIO
+#define RLLM_STREAM_PRIO 1
+#endif
+constexpr bool STREAM_PRIO = RLLM_STREAM_PRIO != 0;
 constexpr int PF_K = RLLM_PF_K;              // K row-pair steps in flight
 constexpr int PF_V = RLLM_PF_V;              // V blocks in flight
 constexpr float LOG2E = 1.4426950408889634f;
@@ -778,15 +791,14 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(DecodeArgs a) {
 // starts; every piece is counted in a per-row arrival counter and the wave
 // that completes the count merges the row (no second kernel).
 // ---------------------------------------------------------------------------
+// Equal shares of the stream-mode work list: wave w takes items
+// [w * total / nws, (w + 1) * total / nws).
 struct WorkList {
-    int64_t total;   // sum over sequences of ctx blocks, times Hkv
-    __device__ __forceinline__ static int64_t share_begin(int64_t total, int w, int nw) {
-        return static_cast<int64_t>(w) * total / nw;
-    }
+    int64_t total;   // items
+    int nws;
+    __device__ __forceinline__ int64_t share_begin(int w) const { return static_cast<int64_t>(w) * total / nws; }
     // wave whose share holds item x
-    __device__ __forceinline__ static int wave_of(int64_t total, int64_t x, int nw) {
-        return static_cast<int>(((x + 1) * nw - 1) / total);
-    }
+    __device__ __forceinline__ int wave_of(int64_t x) const { return static_cast<int>(((x + 1) * nws - 1) / total); }
 };
 
 // Load that is coherent across the whole device (all XCDs' L2s): an
@@ -806,45 +818,80 @@ __device__ __forceinline__ void publish_partials() {
     __builtin_amdgcn_s_waitcnt(0);
 }
 
-// Counts one published partial towards the row whose first piece lies in wave
-// `owner`.  Returns true in the wave that brings the count to `pieces`: that
-// wave merges the row and resets the counter to zero so the workspace is ready
-// for the next call.
-__device__ __forceinline__ bool arrive_last(uint32_t* arrivals, int owner, int pieces) {
-    uint32_t old = 0;
-    if (lane_id() == 0)
-        old = __hip_atomic_fetch_add(arrivals + owner, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    const bool last = old == static_cast<uint32_t>(pieces - 1);
-    if (last && lane_id() == 0)
-        __hip_atomic_store(arrivals + owner, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return last;
+// A row (s, kv head h) split between waves wa..wb: the tail piece of wave wa
+// (slot 2*wa+1) and the head pieces of waves wa+1..wb (slot 2*w).
+struct SplitRow {
+    int s, h, wa, wb;
+};
+
+// Counts this wave's published pieces of rows r0 and (when two) r1 towards
+// their arrival counters, kept at the row's first wave.  Both counters are
+// incremented before either result is used (one round trip).  last0 / last1:
+// this wave completed the count, so it merges the row and resets the counter
+// to zero (the workspace is then ready for the next call).
+__device__ __forceinline__ void arrive2(uint32_t* arrivals, const SplitRow& r0, const SplitRow& r1, bool two,
+                                        bool& last0, bool& last1) {
+    uint32_t old0 = 0, old1 = 0;
+    if (lane_id() == 0) {
+        old0 = __hip_atomic_fetch_add(arrivals + r0.wa, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (two) old1 = __hip_atomic_fetch_add(arrivals + r1.wa, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    old0 = __builtin_amdgcn_readfirstlane(old0);
+    old1 = __builtin_amdgcn_readfirstlane(old1);
+    last0 = old0 == static_cast<uint32_t>(r0.wb - r0.wa);
+    last1 = two && old1 == static_cast<uint32_t>(r1.wb - r1.wa);
+    if (lane_id() == 0) {
+        if (last0) __hip_atomic_store(arrivals + r0.wa, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (last1) __hip_atomic_store(arrivals + r1.wa, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
-// Log-sum-exp merge of the pieces of row (s, kv head h) split between waves
-// wa..wb: the tail piece of wave wa (slot 2*wa+1) and the head pieces of waves
-// wa+1..wb (slot 2*w).  Pieces hold the normalised output and (max, sum).  The
-// loads of up to MC pieces are in flight together.
+// Log-sum-exp merge of one or two split rows (r1 ignored when !two).  The
+// pieces of both rows form one list whose loads go out MC at a time, so two
+// merges cost the round trips of one.  Pieces hold the normalised output and
+// (max, sum).
 template <int QKIND, int D, int G>
-__device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int s, int h, int wa, int wb) {
+__device__ __forceinline__ void merge_split_rows(const DecodeArgs& a, const SplitRow& r0, const SplitRow& r1,
+                                                 bool two) {
     using qtag = typename QT<QKIND>::tag;
     constexpr int PER_LANE = D / 64;
     constexpr int MC = G * (2 + PER_LANE) <= 16 ? 8 : 4;
     const int lane = lane_id();
-    float M[G], L[G], acc[G][PER_LANE];
+    const int p0 = r0.wb - r0.wa + 1;
+    const int np = p0 + (two ? r1.wb - r1.wa + 1 : 0);
+    float M[2][G], L[2][G], acc[2][G][PER_LANE];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        M[g] = -INFINITY;
-        L[g] = 0.f;
+    for (int r = 0; r < 2; ++r)
 #pragma unroll
-        for (int k = 0; k < PER_LANE; ++k) acc[g][k] = 0.f;
-    }
+        for (int g = 0; g < G; ++g) {
+            M[r][g] = -INFINITY;
+            L[r][g] = 0.f;
+#pragma unroll
+            for (int k = 0; k < PER_LANE; ++k) acc[r][g][k] = 0.f;
+        }
+    auto combine = [&](float (&Mr)[G], float (&Lr)[G], float (&accr)[G][PER_LANE], const float* mp,
+                       const float* lp, const float (*op)[PER_LANE]) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (mp[g] == -INFINITY) continue;   // piece without a valid token
+            const float mn = fmaxf(Mr[g], mp[g]);
+            const float fo = __builtin_amdgcn_exp2f(Mr[g] - mn);   // 0 while M is -inf
+            const float fp = __builtin_amdgcn_exp2f(mp[g] - mn) * lp[g];
+            Lr[g] = Lr[g] * fo + fp;
+#pragma unroll
+            for (int k = 0; k < PER_LANE; ++k) accr[g][k] = fmaf(fp, op[g][k], accr[g][k] * fo);
+            Mr[g] = mn;
+        }
+    };
 #pragma unroll 1
-    for (int w0 = wa; w0 <= wb; w0 += MC) {
+    for (int i0 = 0; i0 < np; i0 += MC) {
         float mp[MC][G], lp[MC][G], op[MC][G][PER_LANE];
 #pragma unroll
         for (int c = 0; c < MC; ++c) {
-            const int w = min(w0 + c, wb);   // past wb: a repeat of wb's piece, not merged
+            const int i = min(i0 + c, np - 1);   // past the list: a repeat of the last piece, not merged
+            const bool second = i >= p0;
+            const int wa = second ? r1.wa : r0.wa;
+            const int w = wa + (second ? i - p0 : i);
             const int64_t slot = 2 * static_cast<int64_t>(w) + (w == wa ? 1 : 0);
             const float* ml = a.part_ml + slot * G * 2;
             const float* po = a.part_out + slot * G * D;
@@ -858,27 +905,23 @@ __device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int s, int 
         }
 #pragma unroll
         for (int c = 0; c < MC; ++c) {
-            if (w0 + c > wb) break;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                if (mp[c][g] == -INFINITY) continue;   // piece without a valid token
-                const float mn = fmaxf(M[g], mp[c][g]);
-                const float fo = __builtin_amdgcn_exp2f(M[g] - mn);   // 0 while M is -inf
-                const float fp = __builtin_amdgcn_exp2f(mp[c][g] - mn) * lp[c][g];
-                L[g] = L[g] * fo + fp;
-#pragma unroll
-                for (int k = 0; k < PER_LANE; ++k) acc[g][k] = fmaf(fp, op[c][g][k], acc[g][k] * fo);
-                M[g] = mn;
-            }
+            if (i0 + c >= np) break;
+            if (i0 + c < p0) combine(M[0], L[0], acc[0], mp[c], lp[c], op[c]);
+            else combine(M[1], L[1], acc[1], mp[c], lp[c], op[c]);
         }
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float inv = L[g] > 0.f ? a.v_scale / L[g] : 0.f;
-        uint16_t* row = static_cast<uint16_t*>(a.out) +
-                        (static_cast<int64_t>(s) * a.num_q_heads + h * G + g) * D;
+    for (int r = 0; r < 2; ++r) {
+        if (r == 1 && !two) break;
+        const SplitRow& row = r == 0 ? r0 : r1;
 #pragma unroll
-        for (int k = 0; k < PER_LANE; ++k) row[lane + 64 * k] = from_f32<qtag>(acc[g][k] * inv);
+        for (int g = 0; g < G; ++g) {
+            const float inv = L[r][g] > 0.f ? a.v_scale / L[r][g] : 0.f;
+            uint16_t* dst = static_cast<uint16_t*>(a.out) +
+                            (static_cast<int64_t>(row.s) * a.num_q_heads + row.h * G + g) * D;
+#pragma unroll
+            for (int k = 0; k < PER_LANE; ++k) dst[lane + 64 * k] = from_f32<qtag>(acc[r][g][k] * inv);
+        }
     }
 }
 
@@ -914,43 +957,66 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(2))) v
         }
     }
 
-    // blocks of sequences 0..c (inclusive scan), sequences 0..63 from registers
-    const int incl_l = wave_scan(nb_l);
+    // The work list: every (sequence, kv head) row with context is ROW_COST
+    // virtual items (its start-up: table, q and pipeline fill, and a window
+    // more) followed by its cache blocks; shares are equal runs of this list,
+    // so a share that starts more rows gets fewer blocks.  Items of
+    // sequences 0..c (inclusive scan), sequences 0..63 from registers.
+    // Rows of equal length (a uniform batch) split evenly without virtual
+    // items (shares then align with the rows); only mixed lengths get them.
+    int nb_min = nb_l > 0 ? nb_l : INT_MAX, nb_max = nb_l;
+    for (int c0 = 64; c0 < nseq; c0 += 64) {
+        const int i = c0 + lane;
+        const int nb = i < nseq ? ctx_blocks(a, i) : 0;
+        if (nb > 0) nb_min = min(nb_min, nb);
+        nb_max = max(nb_max, nb);
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        nb_min = min(nb_min, __shfl_xor(nb_min, off));
+        nb_max = max(nb_max, __shfl_xor(nb_max, off));
+    }
+    const int ROW_COST = __builtin_amdgcn_readfirstlane(nb_max > nb_min ? RLLM_ROW_COST * (A::EB == 1 ? 2 : 1) : 0);
+    const int cnt_l = nb_l > 0 ? nb_l + ROW_COST : 0;   // items of one row of sequence `lane`
+    const int incl_l = wave_scan(cnt_l);
     int64_t total = __builtin_amdgcn_readlane(incl_l, 63);
     for (int c0 = 64; c0 < nseq; c0 += 64) {
         const int i = c0 + lane;
         const int nb = i < nseq ? ctx_blocks(a, i) : 0;
-        total += __builtin_amdgcn_readlane(wave_scan(nb), 63);
+        total += __builtin_amdgcn_readlane(wave_scan(nb > 0 ? nb + ROW_COST : 0), 63);
     }
     total *= hkv;
     // No share may be empty: a cut row counts its pieces as the shares its
     // items span, so there are at most as many shares as items (the grid is
-    // sized from the table width, which can exceed the contexts by far).
+    // sized from the table width, which can exceed the contexts by far).  A
+    // share of virtual items only has no piece and lies in no row's count.
     const int nws = static_cast<int>(min(static_cast<int64_t>(nw), total));
     if (w >= nws) return;
-    const int64_t lo = WorkList::share_begin(total, w, nws);
-    const int64_t hi = WorkList::share_begin(total, w + 1, nws);
+    const WorkList wl{total, nws};
+    const int64_t lo = wl.share_begin(w);
+    const int64_t hi = wl.share_begin(w + 1);
 
     // locate the sequence holding item lo
     int s = 0;
-    int64_t pre = 0;   // blocks of the sequences before s
+    int64_t pre = 0;   // items of the sequences before s, per kv head
     {
         const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < nseq && static_cast<int64_t>(incl_l) * hkv > lo);
         if (hit) {
             const int f = __builtin_ctzll(hit);
             s = f;
-            pre = __builtin_amdgcn_readlane(incl_l, f) - __builtin_amdgcn_readlane(nb_l, f);
+            pre = __builtin_amdgcn_readlane(incl_l, f) - __builtin_amdgcn_readlane(cnt_l, f);
         } else {
             int64_t carry = __builtin_amdgcn_readlane(incl_l, 63);
             for (int c0 = 64; c0 < nseq; c0 += 64) {
                 const int i = c0 + lane;
                 const int nb = i < nseq ? ctx_blocks(a, i) : 0;
-                const int64_t incl = carry + wave_scan(nb);
+                const int cnt = nb > 0 ? nb + ROW_COST : 0;
+                const int64_t incl = carry + wave_scan(cnt);
                 const uint64_t hit2 = __builtin_amdgcn_ballot_w64(i < nseq && incl * hkv > lo);
                 if (hit2) {
                     const int f = __builtin_ctzll(hit2);
                     s = c0 + f;
-                    pre = readlane64(incl, f) - __builtin_amdgcn_readlane(nb, f);
+                    pre = readlane64(incl, f) - __builtin_amdgcn_readlane(cnt, f);
                     break;
                 }
                 carry = readlane64(incl, 63);
@@ -961,34 +1027,44 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(2))) v
     int64_t item = lo;
     int ctx = ctx_of(s);
     int nb = blocks_of(a, ctx);
-    const int64_t rel = item - pre * hkv;
-    int h = static_cast<int>(rel / nb);
-    int b0 = static_cast<int>(rel - static_cast<int64_t>(h) * nb);
+    int h = static_cast<int>((item - pre * hkv) / (nb + ROW_COST));
+    // item of block 0 of row (s, h), past its virtual items
+    int64_t first = pre * hkv + static_cast<int64_t>(h) * (nb + ROW_COST) + ROW_COST;
     // split pieces: the share's first piece (head) and last piece (tail) are
     // the only ones a share boundary can cut
-    struct Split {
-        int s, h, wa, wb;
-    };
-    Split split0{}, split1{};
+    SplitRow split0{}, split1{};
     int nsplit = 0;
+    int windows_done = 0;
+    if constexpr (STREAM_PRIO) __builtin_amdgcn_s_setprio(3);
     A::process(
         a, qp, pl,
         [&](Piece& p) {
-            if (item >= hi) return false;
-            const int b1 = static_cast<int>(min(static_cast<int64_t>(nb), b0 + (hi - item)));
-            p = Piece{s, h, b0, b1, nb, ctx, pre * hkv + static_cast<int64_t>(h) * nb};
-            item += b1 - b0;
-            b0 = 0;
-            if (++h == hkv) {
-                h = 0;
-                pre += nb;
-                do {
-                    ++s;
-                    ctx = s < nseq ? ctx_of(s) : 1;
-                    nb = blocks_of(a, ctx);
-                } while (nb == 0);
+            for (;;) {
+                if (item >= hi) return false;
+                // the share's part of row (s, h): its blocks among items [item, hi)
+                const int64_t row_first = first;
+                const int64_t end = first + nb;
+                const int b0 = static_cast<int>(max(item, row_first) - row_first);
+                const int b1 = static_cast<int>(min(hi, end) - row_first);
+                const int ps = s, ph = h, pnb = nb, pctx = ctx;
+                item = min(hi, end);
+                if (item == end) {   // the next row
+                    first = end + ROW_COST;
+                    if (++h == hkv) {
+                        h = 0;
+                        do {
+                            ++s;
+                            ctx = s < nseq ? ctx_of(s) : 1;
+                            nb = blocks_of(a, ctx);
+                        } while (nb == 0);
+                    }
+                }
+                if (b1 > b0) {
+                    p = Piece{ps, ph, b0, b1, pnb, pctx, row_first};
+                    return true;
+                }
+                // only virtual items of this row are in the share
             }
-            return true;
         },
         [&](const Piece& p, const typename A::State& st) {
             if (p.b0 == 0 && p.b1 == p.nb) {
@@ -998,22 +1074,32 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(2))) v
             // b0 > 0: the wave's first piece (head); else its last (tail)
             const int64_t slot = 2 * static_cast<int64_t>(w) + (p.b0 > 0 ? 0 : 1);
             A::template store_partial<true>(a.part_out + slot * G * D, D, a.part_ml + slot * G * 2, 2, st);
-            const Split sp{p.s, p.h, WorkList::wave_of(total, p.row_item, nws),
-                           WorkList::wave_of(total, p.row_item + p.nb - 1, nws)};
+            const SplitRow sp{p.s, p.h, wl.wave_of(p.row_item), wl.wave_of(p.row_item + p.nb - 1)};
             if (nsplit++ == 0)
                 split0 = sp;
             else
                 split1 = sp;
         },
-        [] {});
+        [&] {
+            if constexpr (STREAM_PRIO) {
+                // the two waves of a SIMD are served oldest first; a wave
+                // that has attended fewer windows issues first instead, so
+                // they progress together
+                ++windows_done;
+                if (windows_done == 1) __builtin_amdgcn_s_setprio(2);
+                else if (windows_done == 2) __builtin_amdgcn_s_setprio(1);
+                else if (windows_done == 3) __builtin_amdgcn_s_setprio(0);
+            }
+        });
     // Arrivals wait until the share is done: publishing a partial drains the
     // wave's loads, which mid-share would include the next window's.
     if (nsplit > 0) {
         publish_partials();
-        if (arrive_last(a.arrivals, split0.wa, split0.wb - split0.wa + 1))
-            merge_split_row<QKIND, D, G>(a, split0.s, split0.h, split0.wa, split0.wb);
-        if (nsplit > 1 && arrive_last(a.arrivals, split1.wa, split1.wb - split1.wa + 1))
-            merge_split_row<QKIND, D, G>(a, split1.s, split1.h, split1.wa, split1.wb);
+        bool last0, last1;
+        arrive2(a.arrivals, split0, split1, nsplit > 1, last0, last1);
+        if (last0 && last1) merge_split_rows<QKIND, D, G>(a, split0, split1, true);
+        else if (last0) merge_split_rows<QKIND, D, G>(a, split0, split0, false);
+        else if (last1) merge_split_rows<QKIND, D, G>(a, split1, split1, false);
     }
 }
 
