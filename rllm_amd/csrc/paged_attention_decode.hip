@@ -925,8 +925,11 @@ __device__ __forceinline__ void merge_split_rows(const DecodeArgs& a, const Spli
     }
 }
 
+#ifndef RLLM_STREAM_WAVES_PER_EU
+#define RLLM_STREAM_WAVES_PER_EU 2
+#endif
 template <int QKIND, int KVKIND, int D, int G, int WPB>
-__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(2))) void decode_stream_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(RLLM_STREAM_WAVES_PER_EU))) void decode_stream_kernel(DecodeArgs a) {
     using A = Attn<QKIND, KVKIND, D, G>;
     using qtag = typename QT<QKIND>::tag;
     __shared__ __align__(16) typename A::QP qp_all[WPB];
