@@ -75,6 +75,11 @@ template <> struct Mfma<KIND_BF16> {
     __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
     }
+    // acc + lo + hi of a packed pair (v_dot2_f32_bf16 against (1, 1))
+    __device__ __forceinline__ static float dot2_ones(uint32_t w, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                               __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+    }
 };
 template <> struct Mfma<KIND_F16> {
     using vec = f16x8;
@@ -84,6 +89,11 @@ template <> struct Mfma<KIND_F16> {
     __device__ __forceinline__ static uint16_t bits(float f) { return f32_to_f16_bits(f); }
     __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+    }
+    // acc + lo + hi of a packed pair (v_dot2_f32_f16 against (1, 1))
+    __device__ __forceinline__ static float dot2_ones(uint32_t w, float acc) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3c003c00u), acc,
+                                      false);
     }
 };
 
@@ -337,24 +347,63 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 
         // ---- S^T = K Q^T ----
         f32x4 st[PF_NBT][2];  // [t tile][m tile]
+        auto scores = [&]() {
 #pragma unroll
-        for (int tt = 0; tt < PF_NBT; ++tt) {
-            st[tt][0] = st[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int tt = 0; tt < PF_NBT; ++tt) {
+                st[tt][0] = st[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int k = 0; k < NKS; ++k) {
-                const v4i16 k0 = k_rows4(bc, tt, 32 * k + 8 * lq);
-                const v4i16 k1 = k_rows4(bc, tt, 32 * k + 8 * lq + 4);
-                const vec ka = __builtin_bit_cast(vec, __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7));
-                st[tt][0] = M::mma(ka, qreg[0][k], st[tt][0]);
-                st[tt][1] = M::mma(ka, qreg[1][k], st[tt][1]);
+                for (int k = 0; k < NKS; ++k) {
+                    const v4i16 k0 = k_rows4(bc, tt, 32 * k + 8 * lq);
+                    const v4i16 k1 = k_rows4(bc, tt, 32 * k + 8 * lq + 4);
+                    const vec ka = __builtin_bit_cast(vec, __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7));
+                    st[tt][0] = M::mma(ka, qreg[0][k], st[tt][0]);
+                    st[tt][1] = M::mma(ka, qreg[1][k], st[tt][1]);
+                }
             }
-        }
+        };
+        scores();
 
         // ---- online softmax; lane owns query row lr of each m tile.  Both m
         // tiles are handled in one branch so their dependency chains
         // interleave ----
         constexpr int NE = 4 * PF_NBT;
-        float p[2][NE], m_new[2];
+        uint32_t pk[2][2 * PF_NBT];
+        // Fast path, for tiles every row sees whole once every row has a
+        // running max: the weights are taken against that max as it stands,
+        // p = 2^(s c - m), with no tile max, no rescale of the output and no
+        // cross-lane step.  It is accepted when no lane's weights sum past
+        // 2^8 (then no weight exceeds 2^8, and the output and the sum keep
+        // one common scale); otherwise the scores are computed again and the
+        // tile takes the exact update below (rare: a max that jumps by 2^8).
+        // The weights replace the scores in place and the sum is taken over
+        // the 16-bit weights that multiply V.
+        bool fast = false;
+        if (full && !__builtin_amdgcn_ballot_w64(m_run[0] == -INFINITY || m_run[1] == -INFINITY)) {
+            float ps[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                float acc_s = 0.f;
+#pragma unroll
+                for (int e = 0; e < 2 * PF_NBT; ++e) {
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(st[(2 * e) >> 2][mt][(2 * e) & 3], c, -m_run[mt]));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(st[(2 * e + 1) >> 2][mt][(2 * e + 1) & 3], c, -m_run[mt]));
+                    pk[mt][e] = M::pack2(p0, p1);
+                    acc_s = M::dot2_ones(pk[mt][e], acc_s);
+                }
+                ps[mt] = acc_s;
+            }
+            fast = !__builtin_amdgcn_ballot_w64(!(ps[0] <= 256.f && ps[1] <= 256.f));
+            if (fast) {
+                l_run[0] += ps[0];
+                l_run[1] += ps[1];
+            } else {
+                scores();
+            }
+        }
+        if (!fast) {
+        // exact update: the tile max moves the running max; scores turn into
+        // weights in place (st), so no second copy of the tile is live
+        float m_new[2];
         if (full) {
             // no mask; scale > 0, so the max of the raw scores gives the max
             float mx[2];
@@ -370,9 +419,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
             for (int e = 0; e < NE; ++e)
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt)
-                    p[mt][e] = __builtin_amdgcn_exp2f(fmaf(st[e >> 2][mt][e & 3], c, -m_new[mt]));
+                    st[e >> 2][mt][e & 3] = __builtin_amdgcn_exp2f(fmaf(st[e >> 2][mt][e & 3], c, -m_new[mt]));
         } else {
-            float sv[2][NE], mx[2] = {-INFINITY, -INFINITY};
+            float mx[2] = {-INFINITY, -INFINITY};
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -380,29 +429,30 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
                     const int tt = e >> 2, r = e & 3;
                     const int t = t_base + 16 * tt + 4 * lq + r;
                     const bool ok = pbv[tt] >= 0 && t <= pos[mt] && t < kv_end;
-                    sv[mt][e] = ok ? st[tt][mt][r] * c : -INFINITY;
-                    mx[mt] = fmaxf(mx[mt], sv[mt][e]);
+                    st[tt][mt][r] = ok ? st[tt][mt][r] * c : -INFINITY;
+                    mx[mt] = fmaxf(mx[mt], st[tt][mt][r]);
                 }
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
                 m_new[mt] = fmaxf(m_run[mt], xor_max_16_32(mx[mt]));
                 const bool none = m_new[mt] == -INFINITY;
 #pragma unroll
-                for (int e = 0; e < NE; ++e) p[mt][e] = none ? 0.f : __builtin_amdgcn_exp2f(sv[mt][e] - m_new[mt]);
+                for (int e = 0; e < NE; ++e)
+                    st[e >> 2][mt][e & 3] = none ? 0.f : __builtin_amdgcn_exp2f(st[e >> 2][mt][e & 3] - m_new[mt]);
             }
         }
         float alpha[2];
-        uint32_t pk[2][2 * PF_NBT];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             alpha[mt] = m_new[mt] == m_run[mt] ? 1.f : __builtin_amdgcn_exp2f(m_run[mt] - m_new[mt]);
             float psum = 0.f;
 #pragma unroll
-            for (int e = 0; e < NE; ++e) psum += p[mt][e];
+            for (int e = 0; e < 2 * PF_NBT; ++e) {
+                pk[mt][e] = M::pack2(st[(2 * e) >> 2][mt][(2 * e) & 3], st[(2 * e + 1) >> 2][mt][(2 * e + 1) & 3]);
+                psum = M::dot2_ones(pk[mt][e], psum);
+            }
             l_run[mt] = l_run[mt] * alpha[mt] + psum;
             m_run[mt] = m_new[mt];
-#pragma unroll
-            for (int e = 0; e < 2 * PF_NBT; ++e) pk[mt][e] = M::pack2(p[mt][2 * e], p[mt][2 * e + 1]);
         }
         // the output accumulators change only when some row's max moved
         if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f)) {
@@ -410,6 +460,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) o[mt][dt] *= alpha[mt];
+        }
         }
 
         // ---- O^T = V^T P^T: k-step kk covers t tiles 2kk and 2kk+1 ----
