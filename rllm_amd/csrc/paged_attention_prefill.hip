@@ -217,12 +217,22 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     // this workgroup's KV tiles [t_lo, t_hi): one contiguous share per split
     const int per_split = (ntiles + a.splits - 1) / a.splits;
     const int t_lo = min(ntiles, split * per_split), t_hi = min(ntiles, t_lo + per_split);
-    // the block table is read-only for the kernel's lifetime: reading it
-    // through the constant address space gives scalar loads (wave-uniform
-    // entries), which wait on their own counter instead of behind the
-    // staging loads in flight
-    using cint_ptr = const __attribute__((address_space(4))) int32_t*;
-    const cint_ptr bt = (cint_ptr)(a.block_tables + static_cast<int64_t>(s) * a.max_blocks);
+    // Block-table entries come in by vector loads, one tile ahead: lane l < 8
+    // of `bte` holds the entry of block l of tiles (t, t+1), -1 past the
+    // context.  (Scalar loads of the table would share the LDS reads' counter
+    // and turn every wait for an LDS operand into a full drain.)
+    const int32_t* bt_row = a.block_tables + static_cast<int64_t>(s) * a.max_blocks;
+    // raw entries of tiles (tile, tile + 1) in lanes 0..7 (clamped index; the
+    // context test is applied where an entry is used, so nothing waits for
+    // the load before then)
+    auto table_pair = [&](int tile) -> int {
+        return bt_row[min(tile * PF_NBT + (lane & (2 * PF_NBT - 1)), a.max_blocks - 1)];
+    };
+    // entry b of tiles (tile, tile + 1) from `raw`, -1 past the context
+    auto table_entry = [&](int raw, int tile, int b) -> int {
+        const int v = __builtin_amdgcn_readlane(raw, b);
+        return (tile * PF_NBT + b) * PF_BS < kv_end ? v : -1;
+    };
     const int64_t head_elems = static_cast<int64_t>(D) * PF_BS;
 
     // ---- this lane's query rows: m = 32*wave + 16*mt + lr -> (head g, token i) ----
@@ -257,10 +267,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     // lane, lane L of a segment writes bytes 16L..16L+15); V's swizzle is
     // applied by choosing each lane's source half.  FP8 caches are loaded
     // into registers, converted exactly and written to the same layout. ----
-    auto tile_block = [&](int tile, int b) -> int {   // physical block, -1 if none
-        const int blk = tile * PF_NBT + b;
-        return blk * PF_BS < kv_end ? bt[blk] : -1;
-    };
+
     auto v_half = [](int d, int hf) { return hf ^ ((d >> 3) & 1); };   // stored slot of V half hf of row d
     // K rows are permuted within each 16-row group (an involution): the two
     // 16-lane groups of one transposing-read pass read rows 8 apart, which
@@ -268,8 +275,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     auto k_slot = [](int d) { return d ^ (((d >> 3) & 1) << 2); };
     constexpr int FP8_LOADS = FP8 ? D / 32 : 1;     // 8-byte fp8 chunks per lane per tensor
     uint4 kreg[FP8_LOADS], vreg[FP8_LOADS];
-    auto fetch = [&](int tile, int bc) -> void {   // every load is unconditional
-        const int pb = tile_block(tile, wave);
+    // pb: this wave's block of the tile (physical id, -1 if none)
+    auto fetch = [&](int pb, int bc) -> void {   // every load is unconditional
         const int64_t tb = pb >= 0 ? (static_cast<int64_t>(pb) * a.num_kv_heads + h) * head_elems : 0;
         if constexpr (!FP8) {
             const uint16_t* kb = pb >= 0 ? static_cast<const uint16_t*>(a.k_cache) + tb : g_pf_zero;
@@ -321,8 +328,12 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     // q is in registers before the tile loop starts: otherwise its loads are
     // still counted as outstanding on loop entry and every iteration's first
     // MFMA would wait for all loads in flight, the next tile's included
+    int bte = 0;
+    if (t_lo < t_hi) {
+        bte = table_pair(t_lo);
+        fetch(table_entry(bte, t_lo, wave), 0);
+    }
     __builtin_amdgcn_s_waitcnt(0);
-    if (t_lo < t_hi) fetch(t_lo, 0);
     // one KV tile, computed from buffer bc while the next tile is copied into
     // the other buffer
     auto step = [&](int tile, int bc) -> void {
@@ -332,16 +343,19 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         // overwrite)
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tile + 1 < t_hi) fetch(tile + 1, 1 - bc);
-
-        const int t_base = tile * PF_KT;
         int pbv[PF_NBT];
         bool blocks_ok = true;
 #pragma unroll
         for (int b = 0; b < PF_NBT; ++b) {
-            pbv[b] = tile_block(tile, b);
+            pbv[b] = table_entry(bte, tile, b);
             blocks_ok = blocks_ok && pbv[b] >= 0;
         }
+        if (tile + 1 < t_hi) {
+            fetch(table_entry(bte, tile, PF_NBT + wave), 1 - bc);
+            bte = table_pair(tile + 1);   // used by the next tile
+        }
+
+        const int t_base = tile * PF_KT;
         // every row of the wave sees every token of the tile
         const bool full = blocks_ok && t_base + PF_KT <= kv_end && t_base + PF_KT - 1 <= minp && c > 0.f;
 
