@@ -72,6 +72,12 @@ constexpr int SC_TOKENS = SC_BLOCKS * BS;    // 512
 #define RLLM_STREAM_PRIO 1
 #endif
 constexpr bool STREAM_PRIO = RLLM_STREAM_PRIO != 0;
+// The wave in a SIMD's second slot starts one priority level higher, so it
+// wins ties against the first-slot wave, which was dispatched before it
+// (config 2: 114 -> 111-112 us against equal starting levels)
+#ifndef RLLM_PRIO_SLOT
+#define RLLM_PRIO_SLOT 1
+#endif
 constexpr int PF_K = RLLM_PF_K;              // K row-pair steps in flight
 constexpr int PF_V = RLLM_PF_V;              // V blocks in flight
 constexpr float LOG2E = 1.4426950408889634f;
@@ -801,6 +807,14 @@ struct WorkList {
     __device__ __forceinline__ int wave_of(int64_t x) const { return static_cast<int>(((x + 1) * nws - 1) / total); }
 };
 
+// s_setprio with a wave-uniform level 0..3 (the instruction takes an immediate)
+__device__ __forceinline__ void set_prio(int level) {
+    if (level >= 3) __builtin_amdgcn_s_setprio(3);
+    else if (level == 2) __builtin_amdgcn_s_setprio(2);
+    else if (level == 1) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 // Load that is coherent across the whole device (all XCDs' L2s): an
 // agent-scope atomic load bypasses the per-XCD L2 copies.
 __device__ __forceinline__ float load_agent(const float* p) {
@@ -1037,8 +1051,17 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(RLLM_S
     // the only ones a share boundary can cut
     SplitRow split0{}, split1{};
     int nsplit = 0;
-    int windows_done = 0;
-    if constexpr (STREAM_PRIO) __builtin_amdgcn_s_setprio(3);
+    // priority level: starts at 2, or 3 in a SIMD's second wave slot (the
+    // later-dispatched wave wins ties), and drops by one per window attended
+    int prio_level = 2;
+    if constexpr (STREAM_PRIO) {
+#if RLLM_PRIO_SLOT
+        uint32_t hw_id;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID, 0, 4)" : "=s"(hw_id));
+        prio_level += static_cast<int>(hw_id & 1);
+#endif
+        set_prio(prio_level);
+    }
     A::process(
         a, qp, pl,
         [&](Piece& p) {
@@ -1088,10 +1111,7 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(RLLM_S
                 // the two waves of a SIMD are served oldest first; a wave
                 // that has attended fewer windows issues first instead, so
                 // they progress together
-                ++windows_done;
-                if (windows_done == 1) __builtin_amdgcn_s_setprio(2);
-                else if (windows_done == 2) __builtin_amdgcn_s_setprio(1);
-                else if (windows_done == 3) __builtin_amdgcn_s_setprio(0);
+                if (prio_level > 0) set_prio(--prio_level);
             }
         });
     // Arrivals wait until the share is done: publishing a partial drains the
