@@ -1139,8 +1139,14 @@ namespace {
 // one row per wave on a mostly idle GPU (8 x 512-token rows: 14.0 -> 10.1
 // us); splitting long rows finer than 32 blocks costs more in merges than the
 // extra waves gain.
-constexpr int64_t STREAM_BLOCKS_PER_WAVE_MAX = 32;
-constexpr int64_t STREAM_BLOCKS_PER_WAVE_MIN = 8;
+#ifndef RLLM_BLOCKS_PER_WAVE_MAX
+#define RLLM_BLOCKS_PER_WAVE_MAX 32
+#endif
+#ifndef RLLM_BLOCKS_PER_WAVE_MIN
+#define RLLM_BLOCKS_PER_WAVE_MIN 8
+#endif
+constexpr int64_t STREAM_BLOCKS_PER_WAVE_MAX = RLLM_BLOCKS_PER_WAVE_MAX;
+constexpr int64_t STREAM_BLOCKS_PER_WAVE_MIN = RLLM_BLOCKS_PER_WAVE_MIN;
 
 // waves per stream-mode workgroup (each wave still walks its own share); 4 and
 // 8 measured within noise of 1 at the benchmark shapes
