@@ -724,6 +724,9 @@ def main() -> int:
     ap.add_argument("--prefill-seqs", type=int, default=0,
                     help="config 5: time only the first N sequences' chunks (1: one prompt, the small-batch "
                          "path that splits the KV range)")
+    ap.add_argument("--warm-cache", action="store_true",
+                    help="decode: every step reads the same KV pool (L2/MALL keep what fits; config 4a's "
+                         "shared prefix) instead of rotating over pools that do not fit the 256 MB MALL")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
@@ -809,8 +812,11 @@ def main() -> int:
     # rotate over enough pool copies that a step never finds the previous
     # steps' KV in the 256 MB MALL (two copies at full size; more for a share)
     pool_bytes = 2 * pools[0][0].numel() * pools[0][0].element_size()
-    while len(pools) * pool_bytes < 600e6:
-        pools.append((pools[0][0].clone(), pools[0][1].clone()))
+    if args.warm_cache:
+        pools = pools[:1]
+    else:
+        while len(pools) * pool_bytes < 600e6:
+            pools.append((pools[0][0].clone(), pools[0][1].clone()))
     kv_code = rllm_amd.DTYPE_FP8_E4M3 if fp8 else rllm_amd.DTYPE_BF16
     ops.validate_tables(bt, sl, w.num_blocks, w.block_size)
     torch.cuda.synchronize()
@@ -872,6 +878,7 @@ def main() -> int:
                    "head_dim": w.head_dim, "block_size": w.block_size,
                    "sum_context_tokens": int(w.seq_lens.sum()),
                    "max_context": int(w.seq_lens.max()), "partition": args.partition,
+                   "kv_pools": "one (warm cache)" if args.warm_cache else f"{len(pools)} rotated",
                    "parallelism": f"tp{args.tp} share on one GPU" if args.tp > 1 else "single GPU"},
         "seqs_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
