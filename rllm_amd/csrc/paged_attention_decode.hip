@@ -860,81 +860,163 @@ __device__ __forceinline__ void arrive2(uint32_t* arrivals, const SplitRow& r0, 
     }
 }
 
-// Log-sum-exp merge of one or two split rows (r1 ignored when !two).  The
-// pieces of both rows form one list whose loads go out MC at a time, so two
-// merges cost the round trips of one.  Pieces hold the normalised output and
-// (max, sum).
+// Log-sum-exp merge of one or two split rows (r1 ignored when !two).  Pieces
+// hold the normalised output [G][D] and (max, sum) [G][2] as floats; the
+// pieces of both rows form one list, so two merges cost the round trips of
+// one.  All loads are device-coherent (sc1).
+//   1. (max, sum) pairs: lane c*G + g of chunk k holds piece k*MC + c, head g
+//      (one 8-byte load per lane and chunk, up to KA chunks loaded together);
+//      an xor butterfly over the piece bits gives each row's exact max per
+//      head.
+//   2. Outputs, MC pieces per batch (the first batch's loads go out with the
+//      pairs), 16 bytes per lane and load (one instruction covers 256 / D
+//      heads of a piece): lane l handles head
+//      j*HPI + l/LPH, elements 4*(l mod LPH) .. +3, and adds each piece with
+//      weight exp2(max_piece - max_row) * sum_piece (read by readlane from
+//      the pair's lane) in piece order.
+// Every row is thus summed in the same order whether it is merged alone or
+// together with another row, so results do not depend on which wave merges.
 template <int QKIND, int D, int G>
 __device__ __forceinline__ void merge_split_rows(const DecodeArgs& a, const SplitRow& r0, const SplitRow& r1,
                                                  bool two) {
     using qtag = typename QT<QKIND>::tag;
-    constexpr int PER_LANE = D / 64;
-    constexpr int MC = G * (2 + PER_LANE) <= 16 ? 8 : 4;
+    constexpr int LPH = D / 4;                         // lanes per head (4 floats each)
+    constexpr int HPI = 64 / LPH;                      // heads per load instruction
+    constexpr int NI = (G + HPI - 1) / HPI;            // load instructions per piece
+    constexpr int MC = (32 / NI < 64 / G ? 32 / NI : 64 / G) < 16 ? (32 / NI < 64 / G ? 32 / NI : 64 / G) : 16;
+    constexpr int KA = 4;                              // (max, sum) chunks kept in registers
+    static_assert(D % 64 == 0 && MC >= 1 && MC * G <= 64 && MC * NI <= 32, "merge batch shape");
     const int lane = lane_id();
+    const int lh = lane / LPH;                          // head within an instruction
+    const int lc = lane / G, lg = lane % G;             // (max, sum) lanes: piece, head
     const int p0 = r0.wb - r0.wa + 1;
     const int np = p0 + (two ? r1.wb - r1.wa + 1 : 0);
-    float M[2][G], L[2][G], acc[2][G][PER_LANE];
+    // slot of list entry i (clamped: entries past the list repeat the last
+    // piece and are not merged)
+    auto slot_of = [&](int i) -> int64_t {
+        i = min(i, np - 1);
+        const bool second = i >= p0;
+        const int wa = second ? r1.wa : r0.wa;
+        const int w = wa + (second ? i - p0 : i);
+        return 2 * static_cast<int64_t>(w) + (w == wa ? 1 : 0);
+    };
+    auto load_ml = [&](int i0) -> uint64_t {
+        if (lc >= MC) return 0;
+        return __hip_atomic_load(reinterpret_cast<uint64_t*>(a.part_ml + slot_of(i0 + lc) * G * 2 + 2 * lg),
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto m_of = [](uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); };
+    auto s_of = [](uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); };
+    // value of lane c*G + g (g = this output lane's head in instruction j)
+    auto pick = [&](float v, int c, int j) -> float {
+        float x = 0.f;
+#pragma unroll
+        for (int h = 0; h < HPI; ++h) {
+            if (j * HPI + h >= G) break;
+            const float y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), c * G + j * HPI + h));
+            x = (h == 0 || lh == h) ? y : x;
+        }
+        return x;
+    };
+    auto bfly_max = [](float v) {
+#pragma unroll
+        for (int m = G; m < MC * G; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+        return v;
+    };
+
+    // 1. exact row maxima (lane-parallel per head)
+    uint64_t mls[KA];
+    float Mx[2] = {-INFINITY, -INFINITY};
+    auto fold_max = [&](uint64_t v, int i0) {
+        const bool ok = lc < MC && i0 + lc < np;
+        const float m = m_of(v);
+        Mx[0] = fmaxf(Mx[0], bfly_max(ok && i0 + lc < p0 ? m : -INFINITY));
+        if (two) Mx[1] = fmaxf(Mx[1], bfly_max(ok && i0 + lc >= p0 ? m : -INFINITY));
+    };
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    auto load_out = [&](int i0, u32x4 (&op)[MC][NI]) {
+#pragma unroll
+        for (int c = 0; c < MC; ++c) {
+            // lanes past the piece's G heads read beyond num_records: zeros
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                a.part_out + slot_of(i0 + c) * G * D, static_cast<short>(0), G * D * 4, 0x00020000);
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+                op[c][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (j * HPI * D + 4 * lane) * 4, 0, 16 /* sc1 */);
+        }
+    };
+#pragma unroll
+    for (int k = 0; k < KA; ++k) mls[k] = k * MC < np ? load_ml(k * MC) : 0;
+    u32x4 op0[MC][NI];
+    load_out(0, op0);   // the first batch's outputs travel with the (max, sum) pairs
+#pragma unroll
+    for (int k = 0; k < KA; ++k)
+        if (k * MC < np) fold_max(mls[k], k * MC);
+#pragma unroll 1
+    for (int i0 = KA * MC; i0 < np; i0 += MC) fold_max(load_ml(i0), i0);
+
+    // 2. weighted sums in piece order
+    float acc[2][NI][4], Ls[2][NI];
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            M[r][g] = -INFINITY;
-            L[r][g] = 0.f;
+        for (int j = 0; j < NI; ++j) {
+            Ls[r][j] = 0.f;
 #pragma unroll
-            for (int k = 0; k < PER_LANE; ++k) acc[r][g][k] = 0.f;
+            for (int e = 0; e < 4; ++e) acc[r][j][e] = 0.f;
         }
-    auto combine = [&](float (&Mr)[G], float (&Lr)[G], float (&accr)[G][PER_LANE], const float* mp,
-                       const float* lp, const float (*op)[PER_LANE]) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            if (mp[g] == -INFINITY) continue;   // piece without a valid token
-            const float mn = fmaxf(Mr[g], mp[g]);
-            const float fo = __builtin_amdgcn_exp2f(Mr[g] - mn);   // 0 while M is -inf
-            const float fp = __builtin_amdgcn_exp2f(mp[g] - mn) * lp[g];
-            Lr[g] = Lr[g] * fo + fp;
-#pragma unroll
-            for (int k = 0; k < PER_LANE; ++k) accr[g][k] = fmaf(fp, op[g][k], accr[g][k] * fo);
-            Mr[g] = mn;
-        }
-    };
-#pragma unroll 1
-    for (int i0 = 0; i0 < np; i0 += MC) {
-        float mp[MC][G], lp[MC][G], op[MC][G][PER_LANE];
-#pragma unroll
-        for (int c = 0; c < MC; ++c) {
-            const int i = min(i0 + c, np - 1);   // past the list: a repeat of the last piece, not merged
-            const bool second = i >= p0;
-            const int wa = second ? r1.wa : r0.wa;
-            const int w = wa + (second ? i - p0 : i);
-            const int64_t slot = 2 * static_cast<int64_t>(w) + (w == wa ? 1 : 0);
-            const float* ml = a.part_ml + slot * G * 2;
-            const float* po = a.part_out + slot * G * D;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                mp[c][g] = load_agent(ml + 2 * g);
-                lp[c][g] = load_agent(ml + 2 * g + 1);
-#pragma unroll
-                for (int k = 0; k < PER_LANE; ++k) op[c][g][k] = load_agent(po + g * D + lane + 64 * k);
-            }
-        }
+    auto add_batch = [&](int i0, uint64_t mlv, const u32x4 (&op)[MC][NI]) {
+        // this lane's piece weight (0 past the list and for pieces without a
+        // valid token, whose outputs are zero)
+        const float m_l = m_of(mlv);
+        const float mrow = i0 + lc < p0 ? Mx[0] : Mx[1];
+        const float w_l = lc < MC && i0 + lc < np && m_l != -INFINITY
+                              ? __builtin_amdgcn_exp2f(m_l - mrow) * s_of(mlv) : 0.f;
 #pragma unroll
         for (int c = 0; c < MC; ++c) {
             if (i0 + c >= np) break;
-            if (i0 + c < p0) combine(M[0], L[0], acc[0], mp[c], lp[c], op[c]);
-            else combine(M[1], L[1], acc[1], mp[c], lp[c], op[c]);
+            const int r = i0 + c < p0 ? 0 : 1;
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                const float wp = pick(w_l, c, j);
+                float& lr = r == 0 ? Ls[0][j] : Ls[1][j];
+                lr += wp;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float& ar = r == 0 ? acc[0][j][e] : acc[1][j][e];
+                    ar = fmaf(wp, __uint_as_float(op[c][j][e]), ar);
+                }
+            }
         }
+    };
+    add_batch(0, mls[0], op0);
+#pragma unroll 1
+    for (int b = 1; b * MC < np; ++b) {
+        uint64_t mlv;
+        if (b < KA) {
+            mlv = mls[1];
+#pragma unroll
+            for (int k = 2; k < KA; ++k) mlv = b == k ? mls[k] : mlv;
+        } else {
+            mlv = load_ml(b * MC);
+        }
+        u32x4 op[MC][NI];
+        load_out(b * MC, op);
+        add_batch(b * MC, mlv, op);
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         if (r == 1 && !two) break;
         const SplitRow& row = r == 0 ? r0 : r1;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float inv = L[r][g] > 0.f ? a.v_scale / L[r][g] : 0.f;
+        for (int j = 0; j < NI; ++j) {
+            const int g = j * HPI + lh;
+            if (g >= G) continue;
+            const float inv = Ls[r][j] > 0.f ? a.v_scale / Ls[r][j] : 0.f;
             uint16_t* dst = static_cast<uint16_t*>(a.out) +
-                            (static_cast<int64_t>(row.s) * a.num_q_heads + row.h * G + g) * D;
+                            (static_cast<int64_t>(row.s) * a.num_q_heads + row.h * G + g) * D + 4 * (lane % LPH);
 #pragma unroll
-            for (int k = 0; k < PER_LANE; ++k) dst[lane + 64 * k] = from_f32<qtag>(acc[r][g][k] * inv);
+            for (int e = 0; e < 4; ++e) dst[e] = from_f32<qtag>(acc[r][j][e] * inv);   // out is 2-byte aligned
         }
     }
 }
@@ -1117,6 +1199,8 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(RLLM_S
     // Arrivals wait until the share is done: publishing a partial drains the
     // wave's loads, which mid-share would include the next window's.
     if (nsplit > 0) {
+        // the rest is on the critical path of the rows this wave may merge
+        if constexpr (STREAM_PRIO) set_prio(3);
         publish_partials();
         bool last0, last1;
         arrive2(a.arrivals, split0, split1, nsplit > 1, last0, last1);

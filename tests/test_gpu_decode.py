@@ -303,6 +303,24 @@ def test_decode_long_rows_split_over_many_waves(dev, kind):
     assert_close(got, ref, TOL_BF16 if kind == O.BF16 else TOL_FP8, f"long rows kind={kind}")
 
 
+@pytest.mark.parametrize("cfg", [2, 6])
+def test_decode_stream_merge_is_deterministic(dev, cfg):
+    """Which wave merges a split row (the last piece to arrive) and whether it
+    merges one row or two changes from call to call; the merged output must
+    not: every call is bit-identical (config 2: rows in about five pieces;
+    config 6: 16 x 32768, rows in about sixteen)."""
+    w = workloads.config(cfg)
+    q, k, v = workloads.device_tensors(w, dev)
+    bt = torch.from_numpy(w.block_tables).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    log_case(f"decode determinism config {cfg}")
+    first = ops.paged_decode(q, k, v, bt, sl, w.scale)
+    for i in range(6):
+        again = ops.paged_decode(q, k, v, bt, sl, w.scale)
+        torch.cuda.synchronize()
+        assert torch.equal(again, first), f"config {cfg}: call {i + 1} differs from the first"
+
+
 def test_decode_invalid_arguments(dev):
     bt = torch.zeros((2, 2), dtype=torch.int32, device=dev)
     sl = torch.ones(2, dtype=torch.int32, device=dev)
