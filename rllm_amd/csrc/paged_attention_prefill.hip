@@ -79,10 +79,12 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 
 template <int QKIND> struct Mfma;
 template <> struct Mfma<KIND_BF16> {
     using vec = bf16x8;
+    using elem8 = bf16x8;
     __device__ __forceinline__ static f32x16 mma(const vec& a, const vec& b, const f32x16& c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
@@ -94,6 +96,7 @@ template <> struct Mfma<KIND_BF16> {
 };
 template <> struct Mfma<KIND_F16> {
     using vec = f16x8;
+    using elem8 = f16x8;
     __device__ __forceinline__ static f32x16 mma(const vec& a, const vec& b, const f32x16& c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }
@@ -266,7 +269,11 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
         for (int k = 0; k < NKS; ++k) {
             uint4 w = make_uint4(0, 0, 0, 0);
             if (live) w = *reinterpret_cast<const uint4*>(a.q + orow * D + 16 * k + 8 * hl);
-            qreg[k] = __builtin_bit_cast(vec, w);
+            // Q scaled once by scale * log2(e) (rounded to the q type), so the
+            // products give scores in log2 units
+            vec x = __builtin_bit_cast(vec, w);
+            f32x8 y = __builtin_convertvector(x, f32x8) * a.s_scale;
+            qreg[k] = __builtin_convertvector(y, typename M::elem8);
         }
     }
     // smallest position among the wave's rows: tiles wholly at or below it
@@ -343,7 +350,6 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
 #pragma unroll
         for (int e = 0; e < 8; ++e) pk[sh][e] = 0;
     float m_run = -INFINITY, l_run = 0.f;   // m in scaled log2 units; l: this lane's share of the row sum
-    const float c = a.s_scale;
 
     // ---- matrix phase ----
     // K operand: lane l gets K[token][d0 .. d0 + 3] of the token that row
@@ -397,8 +403,13 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) o[dt] = M::mma(vop[b & 1][dt], pb, o[dt]);
         }
+        // S^T starts at -m_run (0 while a row has no max yet): the fast
+        // softmax then takes exp2 of the product directly
+        const float moff = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
-        for (int sh = 0; sh < 2; ++sh) st[sh] = f32x16{};
+        for (int sh = 0; sh < 2; ++sh)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st[sh][i] = -moff;
 #pragma unroll
         for (int k = 0; k < NKS; ++k) {
             if (k + 1 < NKS) load_k(k + 1, kop[(k + 1) & 1]);
@@ -430,16 +441,16 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
     // path was taken. ----
     auto softmax_fast = [&](int t, int pres) __attribute__((always_inline)) -> bool {
         const int t_base = t * PF_KT;
-        const bool full = pres == (1 << PF_NBT) - 1 && t_base + PF_KT <= kv_end && t_base + PF_KT - 1 <= minp &&
-                          c > 0.f;
+        const bool full = pres == (1 << PF_NBT) - 1 && t_base + PF_KT <= kv_end && t_base + PF_KT - 1 <= minp;
         if (!full || __builtin_amdgcn_ballot_w64(m_run == -INFINITY)) return false;
         float acc_a = 0.f, acc_b = 0.f;
 #pragma unroll
         for (int sh = 0; sh < 2; ++sh)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float p0 = __builtin_amdgcn_exp2f(fmaf(st[sh][2 * e], c, -m_run));
-                const float p1 = __builtin_amdgcn_exp2f(fmaf(st[sh][2 * e + 1], c, -m_run));
+                // the products hold score - m_run in log2 units
+                const float p0 = __builtin_amdgcn_exp2f(st[sh][2 * e]);
+                const float p1 = __builtin_amdgcn_exp2f(st[sh][2 * e + 1]);
                 pk[sh][e] = M::pack2(p0, p1);
                 acc_a += p0;
                 acc_b += p1;
@@ -454,21 +465,23 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
     // weight); the output and the sum are rescaled where the max moved
     auto softmax_exact = [&](int t, int pres) __attribute__((always_inline)) -> void {
         const int t_base = t * PF_KT;
-        const bool full = pres == (1 << PF_NBT) - 1 && t_base + PF_KT <= kv_end && t_base + PF_KT - 1 <= minp &&
-                          c > 0.f;
+        const bool full = pres == (1 << PF_NBT) - 1 && t_base + PF_KT <= kv_end && t_base + PF_KT - 1 <= minp;
+        // the products hold score - moff (log2 units), as the matrix phase set them
+        const float moff = m_run == -INFINITY ? 0.f : m_run;
         float m_new;
         if (full) {
-            // no mask; c > 0, so the max of the raw scores gives the max
+            // no mask
             float mx = st[0][0];
 #pragma unroll
             for (int sh = 0; sh < 2; ++sh)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[sh][i]);
-            m_new = fmaxf(m_run, xor_max_32(mx) * c);
+            m_new = fmaxf(m_run, xor_max_32(mx) + moff);
+            const float shift = moff - m_new;
 #pragma unroll
             for (int sh = 0; sh < 2; ++sh)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) st[sh][i] = __builtin_amdgcn_exp2f(fmaf(st[sh][i], c, -m_new));
+                for (int i = 0; i < 16; ++i) st[sh][i] = __builtin_amdgcn_exp2f(st[sh][i] + shift);
         } else {
             float mx = -INFINITY;
 #pragma unroll
@@ -478,7 +491,7 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
                     const int blk = 2 * sh + (i >> 3);
                     const int tok = t_base + 16 * blk + 8 * hl + (i & 7);
                     const bool ok = ((pres >> blk) & 1) && tok <= pos && tok < kv_end;
-                    st[sh][i] = ok ? st[sh][i] * c : -INFINITY;
+                    st[sh][i] = ok ? st[sh][i] + moff : -INFINITY;
                     mx = fmaxf(mx, st[sh][i]);
                 }
             m_new = fmaxf(m_run, xor_max_32(mx));
@@ -759,6 +772,12 @@ int32_t prefill_impl(void* out, const void* q, const void* kc, const void* vc, c
     const bool fp8 = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
     a.s_scale = scale * PF_LOG2E * (fp8 ? k_scale : 1.f);
     a.v_scale = fp8 ? v_scale : 1.f;
+    // the kernel multiplies the queries by s_scale in the q type: f16 queries
+    // could overflow when it exceeds 1 (bf16 has the float range); that rare
+    // case runs on the shape-general kernel, which scales the fp32 scores
+    if (q_dtype == KIND_F16 && !(std::fabs(a.s_scale) <= 1.f))
+        return generic_attention(out, q, kc, vc, bt, seq_lens, qsl, num_seqs, num_tokens, hq, hkv, d, bs, maxb,
+                                 scale, q_dtype, kv_dtype, k_scale, v_scale, as_stream(stream));
 
     // an upper bound of the query tiles: sum_s ceil(n_s/QT) <= T/QT + num_seqs
     const int64_t QT = PP_ROWS / G;

@@ -89,6 +89,24 @@ def test_prefill_shapes_vs_oracle(dev, D, G, kind):
     assert rl2 < 1e-2
 
 
+@pytest.mark.parametrize("kind", [O.BF16, O.F16])
+@pytest.mark.parametrize("scale", [1.0, 0.75, -0.3])
+def test_prefill_large_and_negative_scales_vs_oracle(dev, kind, scale):
+    """The queries are multiplied by scale * log2(e) in the q type before the
+    products: scale 1 (c = 1.44) and 0.75 (c = 1.08) put f16 queries on the
+    shape-general kernel (no f16 overflow), bf16 stays on the matrix kernel;
+    a negative scale flips which tokens dominate."""
+    rng = np.random.default_rng(91 + kind)
+    hkv, G, D = 2, 4, 128
+    q, k, v, bt, sl, qsl = make_case(rng, [70, 5, 140], [100, 33, 0], hkv * G, hkv, D)
+    q *= 0.25   # keep the softmax from collapsing onto one token at scale 1
+    qb, kb, vb = O.encode(q, kind), O.encode(k, kind), O.encode(v, kind)
+    ref = O.paged_attention_prefill(qb, kind, kb, vb, kind, bt, sl, qsl, scale, precision=1)
+    got = run_prefill(dev, qb, kind, kb, vb, kind, bt, sl, qsl, scale, label=f"scale={scale}")
+    rl2 = assert_close(got, ref, TOL_BF16, f"prefill scale={scale} kind={kind}")
+    assert rl2 < 1e-2
+
+
 @pytest.mark.parametrize("fp8", [O.FP8_E4M3, O.FP8_E5M2])
 def test_prefill_fp8_kv_vs_oracle(dev, fp8):
     rng = np.random.default_rng(300 + fp8)
