@@ -196,6 +196,7 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
     constexpr bool FP8 = KVKIND == KIND_FP8_E4M3 || KVKIND == KIND_FP8_E5M2;
     constexpr int SEGS = D / 32;      // 1 KiB (64 lanes x 16 B) segments of a block's 16-bit tile
     constexpr int FP8_LOADS = FP8 ? D / 32 : 1;   // 8-byte fp8 chunks per lane of one block
+    static_assert(FP8 || SEGS == 2 || SEGS == 4, "copy count per tile");
 
     // buffer t mod 3 (counted from the workgroup's first tile) holds K of
     // tile t and V of tile t-1; the buffer is chosen at run time, and the
@@ -523,10 +524,10 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
     // group 0 and tile t's products for group 1.  Each wave runs products,
     // barrier, softmax, barrier per tile, group 1 one phase late, so every
     // wave passes the same number of barriers (one before the loop, two per
-    // tile, one more).  As its softmax phase of tile t ends, group 0 waits
-    // for the copies into buffer t+1 (issued a tile earlier) and issues
-    // those of K_{t+2} and V_{t+1} into buffer t+2, last read in phase 2t-1:
-    // they have two phases to land. ----
+    // tile, one more).  As its softmax phase of tile t starts, group 0
+    // issues the copies of K_{t+2} and V_{t+1} into buffer t+2 (last read
+    // in phase 2t-1); as that phase ends it waits for those into buffer t+1,
+    // issued a tile earlier. ----
     if (t_lo < t_hi) {
         auto buf_of = [&](int t) __attribute__((always_inline)) -> int { return (t - t_lo) % PP_NBUF; };
         load_entries(t_lo);
@@ -553,27 +554,41 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
 #pragma unroll
             for (int i = tid - 256; i < NZ; i += 256) vz[i] = make_uint4(0, 0, 0, 0);
         }
+        load_entries(t_lo + 1);   // (t_lo + 1, t_lo + 2) for the first copies
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_s_barrier();
         if (grp == 1) __builtin_amdgcn_s_barrier();
-        // first half of tile t: the products from buffer bc, barrier; then
-        // the entries of tiles (t + 1, t + 2) start to load
+        int pres_next = 0;
+        // first half of tile t: the products from buffer bc and the barrier.
+        // Then group 0 copies K_{t+2} and V_{t+1} into buffer t+2 (last read
+        // in phase 2t-1), always (zeros past the range, so their number is
+        // fixed), with the entries (t+1, t+2) loaded a tile earlier; fp8
+        // caches first convert into buffer t+1 the registers loaded a tile
+        // earlier.  Issued as the softmax phase starts, the copies overlap its
+        // arithmetic and have three phases to land; the entries of the next
+        // pair start to load.
         auto tile_front = [&](int t, int bc) __attribute__((always_inline)) -> void {
             mphase(bc);
             __builtin_amdgcn_s_barrier();
-            load_entries(t + 1);
-        };
-        // second half, after the softmax of tile t (fp8: the registers
-        // loaded a tile earlier are converted into LDS, then reloaded)
-        auto tile_back = [&](int t) __attribute__((always_inline)) -> void {
-            pres = presence(t + 1);
             if (grp == 0) {
-                __builtin_amdgcn_s_waitcnt(0);
                 stage(true, buf_of(t + 1));
                 stage(false, buf_of(t + 1));
-                if (t + 2 < t_hi) fetch(true, entry(t + 1, PF_NBT + my_blk), buf_of(t + 2));
-                if (t + 1 < t_hi) fetch(false, entry(t + 1, my_blk), buf_of(t + 2));
-                if constexpr (FP8) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the stage writes
+                fetch(true, t + 2 < t_hi ? entry(t + 1, PF_NBT + my_blk) : -1, buf_of(t + 2));
+                fetch(false, t + 1 < t_hi ? entry(t + 1, my_blk) : -1, buf_of(t + 2));
+            }
+            pres_next = presence(t + 1);
+            load_entries(t + 2);
+        };
+        // second half, after the softmax of tile t: group 0 waits for the
+        // writes into buffer t+1 (16-bit: the copies issued a tile earlier,
+        // which have landed once only this tile's remain in flight; fp8: the
+        // conversions of this phase), then the barrier
+        auto tile_back = [&](int t) __attribute__((always_inline)) -> void {
+            pres = pres_next;
+            if (grp == 0) {
+                if constexpr (FP8) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                else if constexpr (SEGS == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
             }
             __builtin_amdgcn_s_barrier();
         };
@@ -601,7 +616,10 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
         }
         // V of the last tile is in buffer t_hi
         pv(buf_of(t_hi));
-        if (grp == 0) __builtin_amdgcn_s_barrier();
+        if (grp == 0) {
+            __builtin_amdgcn_s_waitcnt(0);   // no copy in flight at exit
+            __builtin_amdgcn_s_barrier();
+        }
     }
 
     // ---- normalise and store: lane holds out[row][32dt + 8jj + 4hl + 0..3] ----
