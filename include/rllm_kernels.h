@@ -129,7 +129,9 @@ int32_t rllm_paged_attention_decode_bf16_sync(uint16_t *output, const uint16_t *
  *   partition_size  0 = automatic (stream split: every resident wave takes an
  *             equal share of all sequences' cache blocks; a sequence cut
  *             between waves is merged by the last wave to finish a piece of
- *             it, in the same kernel), < 0 = single pass (one wave per
+ *             it, in the same kernel, summing the pieces in a fixed order,
+ *             so repeated calls on the same inputs return the same bits
+ *             whichever wave merges), < 0 = single pass (one wave per
  *             sequence and kv head), > 0 = context tokens per split-K
  *             partition (a multiple of 512; a second kernel merges)
  *   workspace, workspace_bytes  split-K scratch of at least
