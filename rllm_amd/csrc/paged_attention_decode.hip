@@ -1279,8 +1279,14 @@ int max_resident_waves() {
 
 int64_t stream_waves(int64_t num_seqs, int64_t hkv, int64_t max_blocks, int64_t resident) {
     const int64_t work_bound = num_seqs * hkv * max_blocks;
-    const int64_t per_wave =
+    int64_t per_wave =
         std::min(STREAM_BLOCKS_PER_WAVE_MAX, std::max(STREAM_BLOCKS_PER_WAVE_MIN, max_blocks / 4));
+    // at least one wave per SIMD (half the resident bound) where the table
+    // holds enough work: a small batch (one GPU's tensor-parallel share) then
+    // keeps enough loads in flight
+    const int64_t half = resident / 2;
+    if (half > 0)
+        per_wave = std::min(per_wave, std::max(STREAM_BLOCKS_PER_WAVE_MIN, (work_bound + half - 1) / half));
     int64_t nw = (work_bound + per_wave - 1) / per_wave;
     if (nw > resident) nw = resident;
     return nw < 1 ? 1 : nw;
