@@ -1232,12 +1232,12 @@ namespace {
 constexpr int64_t STREAM_BLOCKS_PER_WAVE_MAX = RLLM_BLOCKS_PER_WAVE_MAX;
 constexpr int64_t STREAM_BLOCKS_PER_WAVE_MIN = RLLM_BLOCKS_PER_WAVE_MIN;
 
-// waves per stream-mode workgroup (each wave still walks its own share); 4 and
-// 8 measured within noise of 1 at the benchmark shapes
-#ifndef RLLM_STREAM_WPB
-#define RLLM_STREAM_WPB 1
-#endif
-constexpr int STREAM_WPB = RLLM_STREAM_WPB;
+// Waves per stream-mode workgroup (each wave still walks its own share).  A
+// launch of at least 4 waves per CU uses workgroups of 4, which put one wave
+// on each SIMD of a CU (TP-8 share of config 2: 25.8 -> 23.6 us; config 2
+// unchanged); smaller launches use single-wave workgroups, which spread over
+// all CUs (config 1: 256 waves).
+constexpr int STREAM_WPB_WIDE = 4;
 
 enum class Mode { Stream, Partitioned };
 
@@ -1266,6 +1266,14 @@ int resident_waves(const void* kernel, int wpb) {
     const int n = cus * per_cu * wpb;
     g_occ[{dev, kernel}] = n;
     return n;
+}
+
+// compute units of the current device (0 on failure)
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return cus;
 }
 
 // hardware bound on resident 64-lane waves (sizes the stream workspace)
@@ -1326,14 +1334,16 @@ bool make_partition_plan(int64_t num_seqs, int64_t num_q_heads, int64_t head_dim
 // the kernels of one (q type, kv type, head_dim, group size) instantiation
 struct Kernels {
     const void* part;
-    const void* stream;
+    const void* stream;    // one wave per workgroup
+    const void* stream4;   // STREAM_WPB_WIDE waves per workgroup
     const void* reduce;
 };
 
 template <int QKIND, int KVKIND, int D, int G>
 Kernels kernels_of() {
     return {reinterpret_cast<const void*>(&decode_kernel<QKIND, KVKIND, D, G>),
-            reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB>),
+            reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, 1>),
+            reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB_WIDE>),
             reinterpret_cast<const void*>(&decode_reduce_kernel<QKIND, D>)};
 }
 
@@ -1403,7 +1413,7 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
 
     Plan plan;
     if (partition_size == 0) {
-        const int res = resident_waves(kern.stream, STREAM_WPB);
+        const int res = resident_waves(kern.stream, 1);
         if (res <= 0) return (int32_t)hipErrorInvalidDeviceFunction;
         plan.mode = Mode::Stream;
         const int max_waves = max_resident_waves();
@@ -1467,8 +1477,13 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
     hipStream_t st = as_stream(stream);
     int32_t rc;
     if (plan.mode == Mode::Stream) {
-        rc = launch(kern.stream, dim3(static_cast<unsigned>((plan.num_waves + STREAM_WPB - 1) / STREAM_WPB)), a, st,
-                    STREAM_WPB);
+        const int cus = device_cus();
+        if (cus > 0 && plan.num_waves >= STREAM_WPB_WIDE * cus)
+            rc = launch(kern.stream4,
+                        dim3(static_cast<unsigned>((plan.num_waves + STREAM_WPB_WIDE - 1) / STREAM_WPB_WIDE)), a, st,
+                        STREAM_WPB_WIDE);
+        else
+            rc = launch(kern.stream, dim3(static_cast<unsigned>(plan.num_waves)), a, st, 1);
     } else {
         rc = launch(kern.part, dim3(static_cast<unsigned>(num_seqs * hkv * plan.max_parts)), a, st);
         if (!rc && plan.max_parts > 1)
