@@ -235,19 +235,30 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
     const int t_lo = min(ntiles, split * per_split), t_hi = min(ntiles, t_lo + per_split);
 
     // ---- block-table entries: scalar loads (block_tables is a.block_tables
-    // as a restrict pointer, so these uniform loads become s_load) of the 8
-    // entries of tiles (tile, tile + 1), issued as a softmax phase starts and
-    // first used as it ends (that phase has no LDS reads, whose waits share
-    // the counter) ----
+    // as a restrict pointer, so these uniform loads become s_load) of the 4
+    // entries of a tile (its presence mask) and of the two entries this
+    // wave copies next (block my_blk of the tile: V; of the tile after: K),
+    // loaded a tile before use.  Indexing by my_blk at load time keeps the
+    // copies free of a per-wave selection among the entries ----
     const int32_t* bt_row = block_tables + static_cast<int64_t>(s) * a.max_blocks;
-    int32_t ent[2 * PF_NBT];
+    int32_t ent[2 * PF_NBT];   // [0, PF_NBT): the tile's entries; PF_NBT: own V; PF_NBT + 1: own K of tile + 1
     auto load_entries = [&](int tile) __attribute__((always_inline)) {
+        const int last = a.max_blocks - 1;
 #pragma unroll
-        for (int i = 0; i < 2 * PF_NBT; ++i) ent[i] = bt_row[min(tile * PF_NBT + i, a.max_blocks - 1)];
+        for (int i = 0; i < PF_NBT; ++i) ent[i] = bt_row[min(tile * PF_NBT + i, last)];
+        ent[PF_NBT] = bt_row[min(tile * PF_NBT + my_blk, last)];
+        ent[PF_NBT + 1] = bt_row[min((tile + 1) * PF_NBT + my_blk, last)];
     };
-    // entry i of (tile, tile + 1) as loaded, -1 when missing or past the context
+    // entry i of the loaded tile, -1 when missing or past the context
     auto entry = [&](int tile, int i) __attribute__((always_inline)) -> int {
         return (tile * PF_NBT + i) * PF_BS < kv_end && ent[i] >= 0 ? ent[i] : -1;
+    };
+    // this wave's copy blocks: V of the loaded tile, K of the one after
+    auto own_v = [&](int tile) __attribute__((always_inline)) -> int {
+        return (tile * PF_NBT + my_blk) * PF_BS < kv_end && ent[PF_NBT] >= 0 ? ent[PF_NBT] : -1;
+    };
+    auto own_k = [&](int tile) __attribute__((always_inline)) -> int {
+        return ((tile + 1) * PF_NBT + my_blk) * PF_BS < kv_end && ent[PF_NBT + 1] >= 0 ? ent[PF_NBT + 1] : -1;
     };
     auto presence = [&](int tile) __attribute__((always_inline)) -> int {
         int p = 0;
@@ -306,19 +317,22 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
     uint2 rawk[FP8_LOADS], rawv[FP8_LOADS];
 #pragma unroll
     for (int i = 0; i < FP8_LOADS; ++i) rawk[i] = rawv[i] = make_uint2(0, 0);
+    // the zero tile's address, computed once (not reloaded in the loop)
+    const uint16_t* zero_src = g_pf_zero;
+    asm volatile("" : "+s"(zero_src));
     // is_k is a literal at every call site; pb < 0 reads zeros
     auto fetch = [&](bool is_k, int pb, int nb) __attribute__((always_inline)) -> void {
         const int64_t tb = static_cast<int64_t>(pb) * blk_elems + head_off;
         if constexpr (!FP8) {
             const uint16_t* src = pb >= 0 ? static_cast<const uint16_t*>(is_k ? a.k_cache : a.v_cache) + tb
-                                          : g_pf_zero;
+                                          : zero_src;
             const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
                 lds_u32(is_k ? &k_lds[nb][my_blk][0][0] : &v_lds[nb][my_blk][0][0]));
 #pragma unroll
             for (int i = 0; i < SEGS; ++i) lds_dma16(is_k ? seg_off_k[i] : seg_off_v[i], src, lds0 + 1024 * i);
         } else {
             const uint8_t* src = pb >= 0 ? static_cast<const uint8_t*>(is_k ? a.k_cache : a.v_cache) + tb
-                                         : reinterpret_cast<const uint8_t*>(g_pf_zero);
+                                         : reinterpret_cast<const uint8_t*>(zero_src);
 #pragma unroll
             for (int i = 0; i < FP8_LOADS; ++i) {
                 const uint2 w = *reinterpret_cast<const uint2*>(src + 8 * (64 * i + lane));
@@ -529,7 +543,6 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
     // in phase 2t-1); as that phase ends it waits for those into buffer t+1,
     // issued a tile earlier. ----
     if (t_lo < t_hi) {
-        auto buf_of = [&](int t) __attribute__((always_inline)) -> int { return (t - t_lo) % PP_NBUF; };
         load_entries(t_lo);
         int pres = presence(t_lo);
         // prologue: K_{t_lo} into buffer 0, K_{t_lo+1} and V_{t_lo} into
@@ -541,8 +554,8 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
                 __builtin_amdgcn_s_waitcnt(0);
                 stage(true, 0);
             }
-            if (t_lo + 1 < t_hi) fetch(true, entry(t_lo, PF_NBT + my_blk), 1);
-            fetch(false, entry(t_lo, my_blk), 1);
+            if (t_lo + 1 < t_hi) fetch(true, own_k(t_lo), 1);
+            fetch(false, own_v(t_lo), 1);
             if constexpr (FP8) {
                 __builtin_amdgcn_s_waitcnt(0);
                 stage(true, 1);
@@ -554,7 +567,7 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
 #pragma unroll
             for (int i = tid - 256; i < NZ; i += 256) vz[i] = make_uint4(0, 0, 0, 0);
         }
-        load_entries(t_lo + 1);   // (t_lo + 1, t_lo + 2) for the first copies
+        load_entries(t_lo + 1);   // tile t_lo + 1 (and K of t_lo + 2) for the first copies
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_s_barrier();
         if (grp == 1) __builtin_amdgcn_s_barrier();
@@ -570,11 +583,13 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
         auto tile_front = [&](int t, int bc) __attribute__((always_inline)) -> void {
             mphase(bc);
             __builtin_amdgcn_s_barrier();
+            const int b1 = bc == PP_NBUF - 1 ? 0 : bc + 1;   // buffer of tile t + 1
+            const int b2 = bc == 0 ? PP_NBUF - 1 : bc - 1;   // buffer of tile t + 2
             if (grp == 0) {
-                stage(true, buf_of(t + 1));
-                stage(false, buf_of(t + 1));
-                fetch(true, t + 2 < t_hi ? entry(t + 1, PF_NBT + my_blk) : -1, buf_of(t + 2));
-                fetch(false, t + 1 < t_hi ? entry(t + 1, my_blk) : -1, buf_of(t + 2));
+                stage(true, b1);
+                stage(false, b1);
+                fetch(true, t + 2 < t_hi ? own_k(t + 1) : -1, b2);
+                fetch(false, t + 1 < t_hi ? own_v(t + 1) : -1, b2);
             }
             pres_next = presence(t + 1);
             load_entries(t + 2);
@@ -597,11 +612,12 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
         // resumes (a rescale inside the loop body makes the register
         // allocator copy the accumulators between two register sets on
         // every tile).
-        int t = t_lo;
+        int t = t_lo, bcur = 0;   // bcur: buffer of tile t
+        auto next_buf = [](int b) { return b == PP_NBUF - 1 ? 0 : b + 1; };
         while (t < t_hi) {
             bool exact = false;
-            for (; t < t_hi; ++t) {
-                tile_front(t, buf_of(t));
+            for (; t < t_hi; ++t, bcur = next_buf(bcur)) {
+                tile_front(t, bcur);
                 if (!softmax_fast(t, pres)) {
                     exact = true;
                     break;
@@ -612,10 +628,11 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
                 softmax_exact(t, pres);
                 tile_back(t);
                 ++t;
+                bcur = next_buf(bcur);
             }
         }
         // V of the last tile is in buffer t_hi
-        pv(buf_of(t_hi));
+        pv(bcur);
         if (grp == 0) {
             __builtin_amdgcn_s_waitcnt(0);   // no copy in flight at exit
             __builtin_amdgcn_s_barrier();
