@@ -133,18 +133,34 @@ __device__ __forceinline__ v4i16 lds_read_tr16(const uint16_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
 }
 
-// 16 bytes per lane from global memory into LDS: lane L reads sbase + voff
-// (wave-uniform base, per-lane byte offset) and writes lds_addr + 16 L
-// (lds_addr wave-uniform).  Issued as inline assembly so that the compiler
-// does not track the copy: it would otherwise make every LDS read of a
-// buffer chosen at run time wait for all copies in flight.  The caller waits
-// for the copies (s_waitcnt vmcnt(0)) and synchronises the workgroup before
-// any wave reads what they wrote.
-__device__ __forceinline__ void lds_dma16(uint32_t voff, const void* sbase, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                 :
-                 : "v"(voff), "s"(sbase), "s"(lds_addr)
-                 : "memory", "m0");
+// NSEG 1 KiB segments from global memory into LDS, 16 bytes per lane each:
+// in segment i lane L reads sbase + voff + 1024 i (wave-uniform base,
+// per-lane byte offset) and writes lds_addr + 1024 i + 16 L (lds_addr
+// wave-uniform), all under one M0 write (the instruction offset applies to
+// both addresses).  Issued as inline assembly so that the compiler does not
+// track the copy: it would otherwise make every LDS read of a buffer chosen
+// at run time wait for all copies in flight.  The caller waits for the
+// copies (s_waitcnt vmcnt) and synchronises the workgroup before any wave
+// reads what they wrote.
+template <int NSEG>
+__device__ __forceinline__ void lds_dma16_segs(uint32_t voff, const void* sbase, uint32_t lds_addr) {
+    static_assert(NSEG == 2 || NSEG == 4, "segments per copy");
+    if constexpr (NSEG == 4)
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\t"
+                     "global_load_lds_dwordx4 %0, %1\n\t"
+                     "global_load_lds_dwordx4 %0, %1 offset:1024\n\t"
+                     "global_load_lds_dwordx4 %0, %1 offset:2048\n\t"
+                     "global_load_lds_dwordx4 %0, %1 offset:3072"
+                     :
+                     : "v"(voff), "s"(sbase), "s"(lds_addr)
+                     : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\t"
+                     "global_load_lds_dwordx4 %0, %1\n\t"
+                     "global_load_lds_dwordx4 %0, %1 offset:1024"
+                     :
+                     : "v"(voff), "s"(sbase), "s"(lds_addr)
+                     : "memory", "m0");
 }
 // LDS byte address of a pointer into a __shared__ array (the low 32 bits of
 // its flat address)
@@ -328,8 +344,7 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
                                           : zero_src;
             const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
                 lds_u32(is_k ? &k_lds[nb][my_blk][0][0] : &v_lds[nb][my_blk][0][0]));
-#pragma unroll
-            for (int i = 0; i < SEGS; ++i) lds_dma16(is_k ? seg_off_k[i] : seg_off_v[i], src, lds0 + 1024 * i);
+            lds_dma16_segs<SEGS>(is_k ? seg_off_k[0] : seg_off_v[0], src, lds0);
         } else {
             const uint8_t* src = pb >= 0 ? static_cast<const uint8_t*>(is_k ? a.k_cache : a.v_cache) + tb
                                          : reinterpret_cast<const uint8_t*>(zero_src);
