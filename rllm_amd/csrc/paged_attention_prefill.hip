@@ -259,11 +259,17 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
     const int32_t* bt_row = block_tables + static_cast<int64_t>(s) * a.max_blocks;
     int32_t ent[2 * PF_NBT];   // [0, PF_NBT): the tile's entries; PF_NBT: own V; PF_NBT + 1: own K of tile + 1
     auto load_entries = [&](int tile) __attribute__((always_inline)) {
-        const int last = a.max_blocks - 1;
+        // one base, small clamped offsets (entries past the table width read
+        // its last entry; they lie past the context and are never used)
+        const int e0 = tile * PF_NBT;
+        const int lim = a.max_blocks - 1 - e0;
+        const int32_t* row = bt_row + min(e0, a.max_blocks - 1);
 #pragma unroll
-        for (int i = 0; i < PF_NBT; ++i) ent[i] = bt_row[min(tile * PF_NBT + i, last)];
-        ent[PF_NBT] = bt_row[min(tile * PF_NBT + my_blk, last)];
-        ent[PF_NBT + 1] = bt_row[min((tile + 1) * PF_NBT + my_blk, last)];
+        for (int i = 0; i < PF_NBT; ++i) ent[i] = row[max(0, min(i, lim))];
+        if (grp == 0) {   // only group 0 copies
+            ent[PF_NBT] = row[max(0, min(my_blk, lim))];
+            ent[PF_NBT + 1] = row[max(0, min(PF_NBT + my_blk, lim))];
+        }
     };
     // entry i of the loaded tile, -1 when missing or past the context
     auto entry = [&](int tile, int i) __attribute__((always_inline)) -> int {
@@ -277,10 +283,13 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
         return ((tile + 1) * PF_NBT + my_blk) * PF_BS < kv_end && ent[PF_NBT + 1] >= 0 ? ent[PF_NBT + 1] : -1;
     };
     auto presence = [&](int tile) __attribute__((always_inline)) -> int {
-        int p = 0;
+        // blocks of the tile before the context end, less those with a
+        // negative id
+        const int nin = min(max((kv_end - tile * PF_KT + PF_BS - 1) / PF_BS, 0), PF_NBT);
+        int neg = 0;
 #pragma unroll
-        for (int b = 0; b < PF_NBT; ++b) p |= (entry(tile, b) >= 0 ? 1 : 0) << b;
-        return p;
+        for (int b = 0; b < PF_NBT; ++b) neg |= (static_cast<uint32_t>(ent[b]) >> 31) << b;
+        return ((1 << nin) - 1) & ~neg;
     };
 
     // ---- this lane's query row: m = 32 * wave + l32 -> (head g, token i) ----
