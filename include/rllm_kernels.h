@@ -126,8 +126,9 @@ int32_t rllm_paged_attention_decode_bf16_sync(uint16_t *output, const uint16_t *
  *   kv_dtype  q_dtype, RLLM_DTYPE_FP8_E4M3 or RLLM_DTYPE_FP8_E5M2
  *   k_scale, v_scale  per-tensor dequantisation scales of an FP8 cache
  *             (cache value = byte value * scale); ignored for 16-bit caches
- *   partition_size  0 = automatic (stream split: every resident wave takes an
- *             equal share of all sequences' cache blocks; a sequence cut
+ *   partition_size  0 = automatic (stream split: up to one wave per SIMD for
+ *             a 16-bit cache, two for FP8, each taking an equal share of all
+ *             sequences' cache blocks; a sequence cut
  *             between waves is merged by the last wave to finish a piece of
  *             it, in the same kernel, summing the pieces in a fixed order,
  *             so repeated calls on the same inputs return the same bits
