@@ -281,7 +281,8 @@ struct Win {
     int wb, we, lnb;
 };
 
-template <int QKIND, int KVKIND, int D, int G>
+// VD: V blocks in flight (PF_V, or fewer for the small-share stream kernel)
+template <int QKIND, int KVKIND, int D, int G, int VD = PF_V>
 struct Attn {
     using dot = Dot<QKIND>;
     using raw_t = typename Seg<KVKIND>::raw;
@@ -295,7 +296,7 @@ struct Attn {
     // K row-pair steps and V blocks in flight: half as many for 8-head groups,
     // whose accumulators take twice the registers
     static constexpr int PFK = G >= 8 ? PF_K / 2 : PF_K;
-    static constexpr int PFV = G >= 8 ? PF_V / 2 : PF_V;   // V blocks in flight
+    static constexpr int PFV = G >= 8 ? VD / 2 : VD;   // V blocks in flight
     // narrowest window: its K walk must still hold PFK row-pair steps
     static constexpr int LNB_MIN = (NKS >> 3) >= PFK ? 2 : (NKS >> 2) >= PFK ? 3 : 5;
     using State = RunState<G, NV>;
@@ -1024,9 +1025,9 @@ __device__ __forceinline__ void merge_split_rows(const DecodeArgs& a, const Spli
 #ifndef RLLM_STREAM_WAVES_PER_EU
 #define RLLM_STREAM_WAVES_PER_EU 2
 #endif
-template <int QKIND, int KVKIND, int D, int G, int WPB>
+template <int QKIND, int KVKIND, int D, int G, int WPB, int VD = PF_V>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(RLLM_STREAM_WAVES_PER_EU))) void decode_stream_kernel(DecodeArgs a) {
-    using A = Attn<QKIND, KVKIND, D, G>;
+    using A = Attn<QKIND, KVKIND, D, G, VD>;
     using qtag = typename QT<QKIND>::tag;
     __shared__ __align__(16) typename A::QP qp_all[WPB];
     __shared__ __align__(16) typename A::PL pl_all[WPB];
@@ -1345,14 +1346,29 @@ struct Kernels {
     const void* part;
     const void* stream;    // one wave per workgroup
     const void* stream4;   // STREAM_WPB_WIDE waves per workgroup
+    const void* stream4_small;   // same with SMALL_SHARE_PF_V V blocks in flight (null if none)
     const void* reduce;
 };
 
+// V blocks in flight of the small-share stream kernel: a launch of at least
+// one wave per SIMD over a 16-bit cache whose table bound (sequences x kv
+// heads x table width) is at most SMALL_SHARE_BLOCKS blocks per wave (one
+// GPU's TP-8 share of config 2: 1024 waves of ~9 blocks) walks each window's
+// V with 2 blocks in flight instead of 4 (25.0 -> 23.8 us); larger shares
+// lose 1-3% with it, FP8 caches 7%.  Built for groups of up to 4 heads.
+constexpr int SMALL_SHARE_PF_V = 2;
+constexpr int64_t SMALL_SHARE_BLOCKS = 16;
+
 template <int QKIND, int KVKIND, int D, int G>
 Kernels kernels_of() {
+    const void* small = nullptr;
+    if constexpr (KVKIND == QKIND && G <= 4)
+        small = reinterpret_cast<const void*>(
+            &decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB_WIDE, SMALL_SHARE_PF_V>);
     return {reinterpret_cast<const void*>(&decode_kernel<QKIND, KVKIND, D, G>),
             reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, 1>),
             reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB_WIDE>),
+            small,
             reinterpret_cast<const void*>(&decode_reduce_kernel<QKIND, D>)};
 }
 
@@ -1488,12 +1504,15 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
     int32_t rc;
     if (plan.mode == Mode::Stream) {
         const int cus = device_cus();
-        if (cus > 0 && plan.num_waves >= STREAM_WPB_WIDE * cus)
-            rc = launch(kern.stream4,
+        if (cus > 0 && plan.num_waves >= STREAM_WPB_WIDE * cus) {
+            const bool small = kern.stream4_small &&
+                               num_seqs * hkv * maxb <= SMALL_SHARE_BLOCKS * plan.num_waves;
+            rc = launch(small ? kern.stream4_small : kern.stream4,
                         dim3(static_cast<unsigned>((plan.num_waves + STREAM_WPB_WIDE - 1) / STREAM_WPB_WIDE)), a, st,
                         STREAM_WPB_WIDE);
-        else
+        } else {
             rc = launch(kern.stream, dim3(static_cast<unsigned>(plan.num_waves)), a, st, 1);
+        }
     } else {
         rc = launch(kern.part, dim3(static_cast<unsigned>(num_seqs * hkv * plan.max_parts)), a, st);
         if (!rc && plan.max_parts > 1)
