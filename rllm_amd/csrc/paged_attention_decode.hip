@@ -1352,12 +1352,14 @@ struct Kernels {
 
 // V blocks in flight of the small-share stream kernel: a launch of at least
 // one wave per SIMD over a 16-bit cache whose table bound (sequences x kv
-// heads x table width) is at most SMALL_SHARE_BLOCKS blocks per wave (one
-// GPU's TP-8 share of config 2: 1024 waves of ~9 blocks) walks each window's
-// V with 2 blocks in flight instead of 4 (25.0 -> 23.8 us); larger shares
-// lose 1-3% with it, FP8 caches 7%.  Built for groups of up to 4 heads.
+// heads x table width) is at most SMALL_SHARE_BLOCKS blocks per wave walks
+// each window's V with 2 blocks in flight instead of 4.  One GPU's TP-8
+// share of config 2 (1024 waves of ~9 blocks): 25.0 -> 23.7 us; its TP-4
+// share (~18 blocks): 34.6 -> 33.5 us.  Larger shares lose 1-3% with it
+// (config 4b, config 1), FP8 caches 7%; 1 V block in flight is slower still.
+// Built for groups of up to 4 heads.
 constexpr int SMALL_SHARE_PF_V = 2;
-constexpr int64_t SMALL_SHARE_BLOCKS = 16;
+constexpr int64_t SMALL_SHARE_BLOCKS = 32;
 
 template <int QKIND, int KVKIND, int D, int G>
 Kernels kernels_of() {

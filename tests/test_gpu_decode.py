@@ -321,25 +321,25 @@ def test_decode_stream_merge_is_deterministic(dev, cfg):
         assert torch.equal(again, first), f"config {cfg}: call {i + 1} differs from the first"
 
 
-@pytest.mark.parametrize("kind", [O.BF16, O.F16])
-def test_decode_tp8_share_small_kernel_vs_oracle(dev, kind):
-    """One GPU's TP-8 share of config 2 (64 sequences, 4 query heads on 1 kv
-    head, ctx U[128, 4096]): about 9 blocks per wave, the launch that takes
-    the small-share stream kernel (2 V blocks in flight); against the oracle,
-    and bit-identical over repeated calls."""
+@pytest.mark.parametrize("tp,kind", [(8, O.BF16), (8, O.F16), (4, O.BF16)])
+def test_decode_tp_share_small_kernel_vs_oracle(dev, tp, kind):
+    """One GPU's TP-8 / TP-4 share of config 2 (64 sequences, 4 query heads
+    per kv head, ctx U[128, 4096]): about 9 / 18 blocks per wave, launches
+    that take the small-share stream kernel (2 V blocks in flight); against
+    the oracle, and bit-identical over repeated calls."""
     import dataclasses
     w = workloads.config(2)
-    w = dataclasses.replace(w, num_q_heads=4, num_kv_heads=1)
+    w = dataclasses.replace(w, num_q_heads=32 // tp, num_kv_heads=8 // tp)
     qb, kb, vb = workloads.host_tensors(w)
     if kind == O.F16:
         # same values re-encoded as f16 (N(0,1) data is well inside its range)
         qb, kb, vb = (O.encode(O.decode(x, O.BF16), O.F16) for x in (qb, kb, vb))
     ref = O.paged_attention_decode(qb, kind, kb, vb, kind, w.block_tables, w.seq_lens, w.scale,
                                    precision=0)
-    got = run_case(dev, qb, kind, kb, vb, kind, w.block_tables, w.seq_lens, w.scale, label="tp8 share")
-    rl2 = assert_close(got, ref, TOL_BF16, f"tp8 share kind={kind}")
+    got = run_case(dev, qb, kind, kb, vb, kind, w.block_tables, w.seq_lens, w.scale, label=f"tp{tp} share")
+    rl2 = assert_close(got, ref, TOL_BF16, f"tp{tp} share kind={kind}")
     assert rl2 < 1e-2, rl2
-    again = run_case(dev, qb, kind, kb, vb, kind, w.block_tables, w.seq_lens, w.scale, label="tp8 again")
+    again = run_case(dev, qb, kind, kb, vb, kind, w.block_tables, w.seq_lens, w.scale, label=f"tp{tp} again")
     assert np.array_equal(again, got)
 
 
