@@ -343,6 +343,24 @@ def test_decode_tp_share_small_kernel_vs_oracle(dev, tp, kind):
     assert np.array_equal(again, got)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("G", [1, 2])
+def test_decode_small_share_kernel_other_groups_vs_oracle(dev, D, G):
+    """Config 2's lengths and tables on one kv head with G = 1 or 2 query
+    heads and head_dim 64 or 128: at most 16 table blocks per wave, which
+    takes the small-share stream kernel of those groups."""
+    import dataclasses
+    w = workloads.config(2)
+    w = dataclasses.replace(w, num_q_heads=G, num_kv_heads=1, head_dim=D)
+    qb, kb, vb = workloads.host_tensors(w)
+    ref = O.paged_attention_decode(qb, O.BF16, kb, vb, O.BF16, w.block_tables, w.seq_lens, w.scale,
+                                   precision=0)
+    got = run_case(dev, qb, O.BF16, kb, vb, O.BF16, w.block_tables, w.seq_lens, w.scale,
+                   label=f"small share G={G} D={D}")
+    rl2 = assert_close(got, ref, TOL_BF16, f"small share G={G} D={D}")
+    assert rl2 < 1e-2, rl2
+
+
 def test_decode_invalid_arguments(dev):
     bt = torch.zeros((2, 2), dtype=torch.int32, device=dev)
     sl = torch.ones(2, dtype=torch.int32, device=dev)
