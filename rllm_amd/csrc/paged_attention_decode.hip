@@ -1286,26 +1286,28 @@ int max_resident_waves() {
     return cus * (thr / 64);
 }
 
-// one_per_simd: 16-bit caches stop at one wave per SIMD (half the resident
-// bound) and give each wave twice the blocks: fewer pieces to publish and
+// simds: SIMDs of the device (4 per CU; 0 if unknown: then half the
+// resident bound stands in for it).
+// one_per_simd: 16-bit caches stop at one wave per SIMD and give each wave
+// twice the blocks of the two the device holds: fewer pieces to publish and
 // merge, and one wave per SIMD keeps enough loads in flight (config 2 110.8 ->
 // 106.2-107.9 us, config 4b 337.8 -> 328.9 us; the shared-prefix batch 68.2 ->
 // 70.2 us).  FP8 caches keep two: a wave spends twice the vector work per
 // byte on converting, which the second wave hides (config 3 196.6 against
 // 233.8 us at one per SIMD).
 int64_t stream_waves(int64_t num_seqs, int64_t hkv, int64_t max_blocks, int64_t resident,
-                     bool one_per_simd) {
+                     int64_t simds, bool one_per_simd) {
     const int64_t work_bound = num_seqs * hkv * max_blocks;
     int64_t per_wave =
         std::min(STREAM_BLOCKS_PER_WAVE_MAX, std::max(STREAM_BLOCKS_PER_WAVE_MIN, max_blocks / 4));
-    // at least one wave per SIMD (half the resident bound) where the table
-    // holds enough work: a small batch (one GPU's tensor-parallel share) then
-    // keeps enough loads in flight
-    const int64_t half = resident / 2;
-    if (half > 0)
-        per_wave = std::min(per_wave, std::max(STREAM_BLOCKS_PER_WAVE_MIN, (work_bound + half - 1) / half));
+    // at least one wave per SIMD where the table holds enough work: a small
+    // batch (one GPU's tensor-parallel share) then keeps enough loads in flight
+    const int64_t per_simd = std::min(resident, simds > 0 ? simds : resident / 2);
+    if (per_simd > 0)
+        per_wave = std::min(per_wave,
+                            std::max(STREAM_BLOCKS_PER_WAVE_MIN, (work_bound + per_simd - 1) / per_simd));
     int64_t nw = (work_bound + per_wave - 1) / per_wave;
-    const int64_t cap = one_per_simd && half > 0 ? half : resident;
+    const int64_t cap = one_per_simd && per_simd > 0 ? per_simd : resident;
     if (nw > cap) nw = cap;
     return nw < 1 ? 1 : nw;
 }
@@ -1446,7 +1448,8 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
         const int max_waves = max_resident_waves();
         if (max_waves < res) return (int32_t)hipErrorInvalidDevice;
         const bool fp8_kv = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
-        plan.num_waves = static_cast<int32_t>(stream_waves(num_seqs, hkv, maxb, res, !fp8_kv));
+        plan.num_waves =
+            static_cast<int32_t>(stream_waves(num_seqs, hkv, maxb, res, 4 * int64_t(device_cus()), !fp8_kv));
         plan.max_waves = max_waves;
         plan.ws_bytes = plan.num_waves > 1 ? stream_ws_bytes(max_waves, plan.num_waves, G, d) : 0;
     } else {
@@ -1632,7 +1635,8 @@ int64_t rllm_paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num
         const int res = max_resident_waves();
         if (res <= 0) return -1;
         // an upper bound over the cache dtypes (FP8 caches may take more waves)
-        const int64_t nw = stream_waves(num_seqs, num_kv_heads, max_num_blocks_per_seq, res, false);
+        const int64_t nw =
+            stream_waves(num_seqs, num_kv_heads, max_num_blocks_per_seq, res, 4 * int64_t(device_cus()), false);
         return nw > 1 ? stream_ws_bytes(res, nw, num_q_heads / num_kv_heads, head_dim) : 0;
     }
     Plan plan;
