@@ -166,13 +166,19 @@ int64_t rllm_paged_attention_decode_workspace_size(int64_t num_seqs, int64_t num
  * under hipGraph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  It calls no hipMalloc, hipFree or allocating library routine:
  * its scratch is one fixed device array of RLLM_DECODE_NOALLOC_SCRATCH_BYTES
- * per GPU, held from library load until the process ends.  A call that would
- * need more scratch than that (rllm_paged_attention_decode_workspace_size
- * gives the figure) returns hipErrorOutOfMemory (2) before any launch; the
- * stream mode of every tuned shape fits.  All calls on one GPU share the
- * array, whatever their stream: calls that overlap in time on one GPU race
- * and must be serialised by the caller.  The first call on a device clears
- * the array's arrival counters with a kernel on `stream`. */
+ * per GPU, held from library load until the process ends.  The array starts
+ * with the stream mode's arrival counters (4 bytes per resident wave of the
+ * device, rounded up to 256: 32 KiB on MI355X); split-K partials
+ * (partition_size > 0) are placed after them, so calls of either mode may
+ * follow each other in any order.  A call that would need more scratch than
+ * the array holds (rllm_paged_attention_decode_workspace_size gives the
+ * figure; split-K adds the counters' bytes to it) returns hipErrorOutOfMemory
+ * (2) before any launch; the stream mode of every tuned shape fits.  All calls
+ * on one GPU share the array, whatever their stream: calls that overlap in
+ * time on one GPU race and must be serialised by the caller.  The first call
+ * on a device clears the counters with a kernel on `stream` and must not be
+ * made under stream capture (it returns hipErrorStreamCaptureUnsupported
+ * then); later calls may be captured. */
 #define RLLM_DECODE_NOALLOC_SCRATCH_BYTES (24ll << 20)
 int32_t rllm_paged_attention_decode_noalloc(void *output, const void *query,
                                             const void *key_cache, const void *value_cache,
