@@ -18,6 +18,13 @@ roofline   = algorithmic bytes / average decode-call duration measured with HIP
 cpu_baseline = the CPU oracle's fp32 decode (C, std threads) on the same
              inputs, timed on this host's cores (oracle/, checker only)
 
+The default run (config 2, no --op / --tp / --partition) adds two more lines
+to the same JSON object, each timed the same way with the same --steps /
+--warmup: "prefill_config5" (the MFMA chunked prefill of config 5, roofline
+against the dense bf16 MFMA peak, with its own CPU baseline) and
+"fp8_decode_config3" (decode over config 3's FP8-E4M3 cache, values drawn on
+the GPU, roofline against HBM peak).  --no-extra leaves them out.
+
 --calibrate-copy-mib N runs the library's block copy over N MiB three times
 after the timed region, so a counter run can scale FETCH_SIZE/WRITE_SIZE.
 """
@@ -139,9 +146,11 @@ def per_launch_ms(step, n, stream):
     return [a.elapsed_time(b) for a, b in ev]
 
 
-def bench_prefill(args, w, lib, dev) -> int:
+def bench_prefill(args, w, lib, dev, kv="bf16", steps=None, warmup=None, calibrate=True) -> dict:
     """Config 5: MFMA chunked prefill (8 seqs x 512 new tokens on 2048 cached),
-    FLOP/s against the dense bf16 MFMA peak."""
+    FLOP/s against the dense bf16 MFMA peak.  Returns the JSON line as a dict."""
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
     import numpy as np
     import torch
 
@@ -150,13 +159,13 @@ def bench_prefill(args, w, lib, dev) -> int:
     t16 = lambda b: torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(dev)
     q = t16(qb)
     kv_code, k_scale, v_scale = rllm_amd.DTYPE_BF16, 1.0, 1.0
-    if args.kv == "bf16":
+    if kv == "bf16":
         pools = [(t16(kb), t16(vb))]
         pools.append((pools[0][0].clone(), pools[0][1].clone()))
     else:
         # the FP8 cache is written by the library's own reshape_and_cache
         from rllm_amd import ops
-        kv_code = rllm_amd.DTYPE_FP8_E4M3 if args.kv == "fp8_e4m3" else rllm_amd.DTYPE_FP8_E5M2
+        kv_code = rllm_amd.DTYPE_FP8_E4M3 if kv == "fp8_e4m3" else rllm_amd.DTYPE_FP8_E5M2
         kf, vf = t16(kb), t16(vb)
         top = 448.0 if kv_code == rllm_amd.DTYPE_FP8_E4M3 else 57344.0
         k_scale, v_scale = float(kf.float().abs().max()) / top, float(vf.float().abs().max()) / top
@@ -187,55 +196,57 @@ def bench_prefill(args, w, lib, dev) -> int:
         if rc:
             raise rllm_amd.KernelError(rc, "rllm_paged_attention_prefill_ex")
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     region_ms = ev0.elapsed_time(ev1)
-    call_ms = per_launch_ms(step, args.steps, stream)
+    call_ms = per_launch_ms(step, steps, stream)
     flops = w.prefill_flops()
-    ms_per_step = wall * 1e3 / args.steps
-    kernel_ms = region_ms / args.steps
+    ms_per_step = wall * 1e3 / steps
+    kernel_ms = region_ms / steps
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     res = {
         "metric": "chunked-prefill paged attention TFLOP/s (MFMA) at 8B shape",
         "value": round(flops / (ms_per_step * 1e-3) / 1e12, 2),
-        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16" if args.kv == "bf16" else f"bf16 (KV {args.kv})",
+        "vs_baseline": None, "dtype": "bf16" if kv == "bf16" else f"bf16 (KV {kv})",
         "data": "synthetic N(0,1) (seeded), random permuted block tables",
-        "config": {"workload": w.name if args.kv == "bf16" else f"{w.name}_{args.kv}kv",
+        "config": {"workload": w.name if kv == "bf16" else f"{w.name}_{kv}kv",
                    "config_index": w.index, "num_seqs": w.num_seqs,
                    "num_tokens": T, "num_q_heads": w.num_q_heads, "num_kv_heads": w.num_kv_heads,
                    "head_dim": w.head_dim, "block_size": w.block_size,
                    "context_per_seq": int(w.seq_lens.max()), "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic(w.name if args.kv == "bf16" else f"{w.name}_{args.kv}kv", "prefill"),
+                     "traffic": measured_traffic(w.name if kv == "bf16" else f"{w.name}_{kv}kv", "prefill"),
                      "kernel_ms": round(kernel_ms, 5),
                      "per_launch_ms_p10_p50_p90": [round(float(np.percentile(call_ms, q)), 5) for q in (10, 50, 90)],
                      "algorithmic_flops": int(flops)},
     }
-    calibrate_copy(args, dev, sh)
+    if calibrate:
+        calibrate_copy(args, dev, sh)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline_prefill(w, qb, kb, vb)
-    print(json.dumps(res), flush=True)
-    return 0
+    del pools, q, out
+    return res
 
 
 def cpu_baseline_prefill(w, qb, kb, vb):
     """The oracle's fp32 chunked prefill (the reference CPU attention with the
     context-offset causal mask) on all usable host cores, over a bounded sample
-    of the batch: the first sequences whose chunks total at least 1/8 of the
-    FLOPs (one of config 5's eight), timed as often as fits in ~10 s."""
+    of the batch: the first sequence's chunk alone (1/8 of config 5's FLOPs,
+    whose eight prompts are equal), after one warm-up run, timed at most 5
+    times and no longer than ~10 s; the median is reported."""
     import numpy as np
     import oracle as O
     cores = _cores()
@@ -692,6 +703,148 @@ def bench_fused(args, w, lib, dev) -> int:
     return 0
 
 
+def bench_decode(args, w, lib, dev, cpu=True, device_values=False, calibrate=True, steps=None,
+                 warmup=None) -> dict:
+    """The decode line of config w (one decode paged-attention call per step
+    over pools rotated past the 256 MB MALL), as a dict: GB/s of algorithmic
+    bytes, roofline against HBM peak, and (cpu) the oracle's CPU baseline on
+    the same host values."""
+    import numpy as np
+    import torch
+
+    import rllm_amd
+    from rllm_amd import ops, workloads
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+
+    def t16(b):
+        return torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(dev)
+
+    fp8 = w.kv_dtype.startswith("fp8")
+    if device_values:
+        # seeded values drawn on the GPU (same distribution, much faster for
+        # the GB-sized pools; no CPU baseline is taken from them)
+        q, kdev, vdev = workloads.device_tensors(w, dev)
+        qb = kb = vb = None
+    else:
+        qb, kb, vb = workloads.host_tensors(w)
+        q = t16(qb)
+        kdev = vdev = None
+    bt = torch.from_numpy(w.block_tables).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    out = torch.empty_like(q)
+    k_scale = v_scale = 1.0
+    pools = []
+    if fp8:
+        # quantise the bf16 pool through the library's own reshape_and_cache
+        kf, vf = (kdev, vdev) if device_values else (t16(kb), t16(vb))
+        k_scale = float(kf.float().abs().max()) / 448.0
+        v_scale = float(vf.float().abs().max()) / 448.0
+        nb = w.num_blocks
+        slots = torch.arange(nb * w.block_size, device=dev, dtype=torch.int64)
+        tok_k = kf.permute(0, 3, 1, 2).reshape(-1, w.num_kv_heads, w.head_dim).contiguous()
+        tok_v = vf.permute(0, 3, 1, 2).reshape(-1, w.num_kv_heads, w.head_dim).contiguous()
+        for _ in range(2):
+            k8 = torch.empty(kf.shape, dtype=torch.uint8, device=dev)
+            v8 = torch.empty_like(k8)
+            ops.reshape_and_cache(tok_k, tok_v, k8, v8, slots, kv_dtype=rllm_amd.DTYPE_FP8_E4M3,
+                                  k_scale=k_scale, v_scale=v_scale)
+            pools.append((k8, v8))
+        del kf, vf, tok_k, tok_v
+    else:
+        kc, vc = (kdev, vdev) if device_values else (t16(kb), t16(vb))
+        pools = [(kc, vc), (kc.clone(), vc.clone())]
+    del kdev, vdev
+    # rotate over enough pool copies that a step never finds the previous
+    # steps' KV in the 256 MB MALL (two copies at full size; more for a share)
+    pool_bytes = 2 * pools[0][0].numel() * pools[0][0].element_size()
+    if args.warm_cache:
+        pools = pools[:1]
+    else:
+        while len(pools) * pool_bytes < 600e6:
+            pools.append((pools[0][0].clone(), pools[0][1].clone()))
+    kv_code = rllm_amd.DTYPE_FP8_E4M3 if fp8 else rllm_amd.DTYPE_BF16
+    ops.validate_tables(bt, sl, w.num_blocks, w.block_size)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    sh = int(stream.cuda_stream)
+    fn = lib.rllm_paged_attention_decode_ex
+    qp, op, btp, slp = q.data_ptr(), out.data_ptr(), bt.data_ptr(), sl.data_ptr()
+    pool_ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in pools]
+
+    def step(i):
+        kp, vp = pool_ptrs[i % len(pool_ptrs)]
+        rc = fn(op, qp, kp, vp, btp, slp, w.num_seqs, w.num_q_heads, w.num_kv_heads, w.head_dim,
+                w.block_size, w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, kv_code, k_scale, v_scale,
+                args.partition, None, 0, sh)
+        if rc:
+            raise rllm_amd.KernelError(rc, "rllm_paged_attention_decode_ex")
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # the timed region: K launches back to back, bracketed by one event pair
+    # on the launch stream (events between launches would add their own gaps)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    region_ms = ev0.elapsed_time(ev1)
+    call_ms = per_launch_ms(step, steps, stream)
+
+    # config 4a aliases one prefix in every table: its roofline counts each
+    # physical block once (the logical figure is reported beside it)
+    nbytes = w.decode_bytes(distinct=(w.index == 4))
+    ms_per_step = wall * 1e3 / steps
+    kernel_ms = region_ms / steps   # average launch duration over the timed region
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+    res = {
+        "metric": "decode paged-attn achieved HBM GB/s (% of peak) + seqs/sec at 8B shape",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3" if fp8 else "bf16",
+        "data": "synthetic N(0,1) (seeded), random permuted block tables",
+        "config": {"workload": w.name, "config_index": w.index, "num_seqs": w.num_seqs,
+                   "num_q_heads": w.num_q_heads, "num_kv_heads": w.num_kv_heads,
+                   "head_dim": w.head_dim, "block_size": w.block_size,
+                   "sum_context_tokens": int(w.seq_lens.sum()),
+                   "max_context": int(w.seq_lens.max()), "partition": args.partition,
+                   "kv_pools": "one (warm cache)" if args.warm_cache else f"{len(pools)} rotated",
+                   "parallelism": f"tp{args.tp} share on one GPU" if args.tp > 1 else "single GPU"},
+        "seqs_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(w.name),
+                     "kernel_ms": round(kernel_ms, 5),
+                     "per_launch_ms_p10_p50_p90": [round(float(np.percentile(call_ms, q)), 5) for q in (10, 50, 90)],
+                     "algorithmic_bytes": nbytes},
+    }
+    if w.index == 4:
+        res["roofline"]["logical_bytes"] = w.decode_bytes()
+    if calibrate:
+        calibrate_copy(args, dev, sh)
+    if cpu and not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(w, qb, kb, vb)
+    del pools, q, out
+    return res
+
+
 def workloads_host(w):
     from rllm_amd import workloads
     return workloads.host_tensors(w)
@@ -728,6 +881,8 @@ def main() -> int:
                     help="decode: every step reads the same KV pool (L2/MALL keep what fits; config 4a's "
                          "shared prefix) instead of rotating over pools that do not fit the 256 MB MALL")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="default run: leave out the config-5 prefill and config-3 FP8 decode lines")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, run the library block copy over this many MiB (counter scaling)")
     args = ap.parse_args()
@@ -770,7 +925,8 @@ def main() -> int:
             w = dataclasses.replace(w, name=f"{w.name}_{n}seq", seq_lens=w.seq_lens[:n].copy(),
                                     block_tables=np.ascontiguousarray(w.block_tables[:n]),
                                     query_lens=w.query_lens[:n].copy())
-        return bench_prefill(args, w, lib, dev)
+        print(json.dumps(bench_prefill(args, w, lib, dev, kv=args.kv)), flush=True)
+        return 0
     if args.tp > 1:
         if w.num_kv_heads % args.tp:
             print(f"--tp {args.tp} does not divide {w.num_kv_heads} kv heads", file=sys.stderr)
@@ -778,122 +934,15 @@ def main() -> int:
         w = dataclasses.replace(w, name=f"{w.name}_tp{args.tp}_share",
                                 num_q_heads=w.num_q_heads // args.tp,
                                 num_kv_heads=w.num_kv_heads // args.tp)
-    fp8 = w.kv_dtype.startswith("fp8")
-    qb, kb, vb = workloads.host_tensors(w)
-
-    def t16(b):
-        return torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(dev)
-
-    q = t16(qb)
-    bt = torch.from_numpy(w.block_tables).to(dev)
-    sl = torch.from_numpy(w.seq_lens).to(dev)
-    out = torch.empty_like(q)
-    k_scale = v_scale = 1.0
-    pools = []
-    if fp8:
-        # quantise the bf16 pool through the library's own reshape_and_cache
-        kf, vf = t16(kb), t16(vb)
-        k_scale = float(kf.float().abs().max()) / 448.0
-        v_scale = float(vf.float().abs().max()) / 448.0
-        nb = w.num_blocks
-        slots = torch.arange(nb * w.block_size, device=dev, dtype=torch.int64)
-        tok_k = kf.permute(0, 3, 1, 2).reshape(-1, w.num_kv_heads, w.head_dim).contiguous()
-        tok_v = vf.permute(0, 3, 1, 2).reshape(-1, w.num_kv_heads, w.head_dim).contiguous()
-        for _ in range(2):
-            k8 = torch.empty(kf.shape, dtype=torch.uint8, device=dev)
-            v8 = torch.empty_like(k8)
-            ops.reshape_and_cache(tok_k, tok_v, k8, v8, slots, kv_dtype=rllm_amd.DTYPE_FP8_E4M3,
-                                  k_scale=k_scale, v_scale=v_scale)
-            pools.append((k8, v8))
-        del kf, vf, tok_k, tok_v
-    else:
-        kc, vc = t16(kb), t16(vb)
-        pools = [(kc, vc), (kc.clone(), vc.clone())]
-    # rotate over enough pool copies that a step never finds the previous
-    # steps' KV in the 256 MB MALL (two copies at full size; more for a share)
-    pool_bytes = 2 * pools[0][0].numel() * pools[0][0].element_size()
-    if args.warm_cache:
-        pools = pools[:1]
-    else:
-        while len(pools) * pool_bytes < 600e6:
-            pools.append((pools[0][0].clone(), pools[0][1].clone()))
-    kv_code = rllm_amd.DTYPE_FP8_E4M3 if fp8 else rllm_amd.DTYPE_BF16
-    ops.validate_tables(bt, sl, w.num_blocks, w.block_size)
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream()
-    sh = int(stream.cuda_stream)
-    fn = lib.rllm_paged_attention_decode_ex
-    qp, op, btp, slp = q.data_ptr(), out.data_ptr(), bt.data_ptr(), sl.data_ptr()
-    pool_ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in pools]
-
-    def step(i):
-        kp, vp = pool_ptrs[i % len(pool_ptrs)]
-        rc = fn(op, qp, kp, vp, btp, slp, w.num_seqs, w.num_q_heads, w.num_kv_heads, w.head_dim,
-                w.block_size, w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, kv_code, k_scale, v_scale,
-                args.partition, None, 0, sh)
-        if rc:
-            raise rllm_amd.KernelError(rc, "rllm_paged_attention_decode_ex")
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # the timed region: K launches back to back, bracketed by one event pair
-    # on the launch stream (events between launches would add their own gaps)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    region_ms = ev0.elapsed_time(ev1)
-    call_ms = per_launch_ms(step, args.steps, stream)
-
-    # config 4a aliases one prefix in every table: its roofline counts each
-    # physical block once (the logical figure is reported beside it)
-    nbytes = w.decode_bytes(distinct=(w.index == 4))
-    ms_per_step = wall * 1e3 / args.steps
-    kernel_ms = region_ms / args.steps   # average launch duration over the timed region
-    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
-    value = nbytes / (ms_per_step * 1e-3) / 1e9
-    res = {
-        "metric": "decode paged-attn achieved HBM GB/s (% of peak) + seqs/sec at 8B shape",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp8_e4m3" if fp8 else "bf16",
-        "data": "synthetic N(0,1) (seeded), random permuted block tables",
-        "config": {"workload": w.name, "config_index": w.index, "num_seqs": w.num_seqs,
-                   "num_q_heads": w.num_q_heads, "num_kv_heads": w.num_kv_heads,
-                   "head_dim": w.head_dim, "block_size": w.block_size,
-                   "sum_context_tokens": int(w.seq_lens.sum()),
-                   "max_context": int(w.seq_lens.max()), "partition": args.partition,
-                   "kv_pools": "one (warm cache)" if args.warm_cache else f"{len(pools)} rotated",
-                   "parallelism": f"tp{args.tp} share on one GPU" if args.tp > 1 else "single GPU"},
-        "seqs_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
-        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(w.name),
-                     "kernel_ms": round(kernel_ms, 5),
-                     "per_launch_ms_p10_p50_p90": [round(float(np.percentile(call_ms, q)), 5) for q in (10, 50, 90)],
-                     "algorithmic_bytes": nbytes},
-    }
-    if w.index == 4:
-        res["roofline"]["logical_bytes"] = w.decode_bytes()
-    calibrate_copy(args, dev, sh)
-    if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(w, qb, kb, vb)
+    res = bench_decode(args, w, lib, dev)
+    if args.config == 2 and args.tp == 1 and args.partition == 0 and not args.warm_cache and not args.no_extra:
+        # the other two headline paths, on the same clock: the MFMA prefill of
+        # config 5 and the FP8-KV decode of config 3, each as its own line
+        torch.cuda.empty_cache()
+        res["prefill_config5"] = bench_prefill(args, workloads.config(5), lib, dev, calibrate=False)
+        torch.cuda.empty_cache()
+        res["fp8_decode_config3"] = bench_decode(args, workloads.config(3), lib, dev, cpu=False,
+                                                 device_values=True, calibrate=False)
     print(json.dumps(res), flush=True)
     return 0
 
