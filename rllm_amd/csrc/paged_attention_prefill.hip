@@ -457,15 +457,35 @@ __global__ __launch_bounds__(PP_THREADS, 1) void prefill_kernel(PrefillArgs a,
             for (int sh = 0; sh < 2; ++sh) st[sh] = M::mma(kop[k & 1][sh], qreg[k], st[sh]);
         }
     };
-    // the V products alone (after the last tile)
+    // The V products alone, after the last tile t_hi - 1.  Only that tile can
+    // hold the block with position ctx - 1 (the workgroup's range ends at or
+    // before the context), whose slots past the context may carry stale bytes
+    // (even NaN or Inf: a block never written in full).  Their weights are 0,
+    // but 0 x NaN is not, so those V words are masked (lane token range
+    // 8 hl .. 8 hl + 7 of the block, two tokens a word).
     auto pv = [&](int bc) __attribute__((always_inline)) -> void {
+        const bool tail = (ctx % PF_BS) != 0 && (ctx - 1) / PF_KT == t_hi - 1;
+        const int tail_b = ((ctx - 1) / PF_BS) % PF_NBT;
+        const int valid = ctx % PF_BS - 8 * hl;   // tokens of this lane's 8 that are in the context
+        uint4 keep;
+        keep.x = valid > 1 ? 0xffffffffu : valid > 0 ? 0x0000ffffu : 0u;
+        keep.y = valid > 3 ? 0xffffffffu : valid > 2 ? 0x0000ffffu : 0u;
+        keep.z = valid > 5 ? 0xffffffffu : valid > 4 ? 0x0000ffffu : 0u;
+        keep.w = valid > 7 ? 0xffffffffu : valid > 6 ? 0x0000ffffu : 0u;
 #pragma unroll
         for (int b = 0; b < PF_NBT; ++b) {
             const vec pb = pv_b(b);
+            const bool mask = tail && b == tail_b;
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
-                const vec va = *reinterpret_cast<const vec*>(&v_lds[bc][b][32 * dt][0] + v_off);
-                o[dt] = M::mma(va, pb, o[dt]);
+                uint4 w = *reinterpret_cast<const uint4*>(&v_lds[bc][b][32 * dt][0] + v_off);
+                if (mask) {
+                    w.x &= keep.x;
+                    w.y &= keep.y;
+                    w.z &= keep.z;
+                    w.w &= keep.w;
+                }
+                o[dt] = M::mma(__builtin_bit_cast(vec, w), pb, o[dt]);
             }
         }
     };

@@ -211,6 +211,25 @@ def test_decode_stale_nan_tail_is_ignored(dev):
     assert_close(got, ref, TOL_BF16, "nan tail")
 
 
+@pytest.mark.parametrize("part", [0, 512])
+def test_decode_fp8_stale_nan_tail_is_ignored(dev, part):
+    """FP8 cache slots past a sequence's context hold the E4M3 NaN byte: output
+    stays finite and equals the oracle's on the clean cache."""
+    rng = np.random.default_rng(19)
+    q, k, v, bt, sl = random_case(rng, 6, 32, 8, 128, (17, 1500))
+    sl[sl % 16 == 0] -= 1   # every context ends inside a block
+    qb = O.encode(q, O.BF16)
+    kb, vb = O.encode(k / 4, O.FP8_E4M3), O.encode(v / 4, O.FP8_E4M3)
+    ref = oracle_ref(qb, O.BF16, kb, vb, O.FP8_E4M3, bt, sl, 0.088, 4.0, 4.0)
+    for s in range(len(sl)):
+        last = bt[s, (sl[s] - 1) // 16]
+        kb[last, :, :, sl[s] % 16:] = 0x7F
+        vb[last, :, :, sl[s] % 16:] = 0x7F
+    got = run_case(dev, qb, O.BF16, kb, vb, O.FP8_E4M3, bt, sl, 0.088, 4.0, 4.0, partition_size=part,
+                   label="fp8 nan-tail")
+    assert_close(got, ref, TOL_FP8, f"fp8 nan tail part={part}")
+
+
 def test_decode_context_clamped_to_table(dev):
     """seq_len beyond max_blocks * block_size reads only the table's blocks."""
     rng = np.random.default_rng(17)

@@ -206,6 +206,41 @@ def test_prefill_config5_full_vs_oracle(dev, kv_kind):
         assert_close(got[rows], dec, (4e-3, 1e-2), f"config5 {which} token vs decode kv={kv_kind}")
 
 
+@pytest.mark.parametrize("kv_kind", [O.BF16, O.FP8_E4M3])
+@pytest.mark.parametrize("nseq", [1, 12])
+def test_prefill_stale_nan_tail_is_ignored(dev, kv_kind, nseq):
+    """Cache slots past a sequence's context (in its last, partly filled block)
+    hold NaN bits, as a reused or never-written block may: those tokens get no
+    weight, and the output must stay finite and equal the oracle's on the clean
+    cache.  One sequence takes the small-batch KV-split path, twelve the
+    unsplit one."""
+    rng = np.random.default_rng(31 + nseq + kv_kind)
+    n_new = rng.integers(1, 90, size=nseq)
+    cached = rng.integers(0, 700, size=nseq)
+    q, k, v, bt, sl, qsl = make_case(rng, n_new, cached, 32, 8, 128)
+    sl[sl % 16 == 0] -= 1   # every context ends inside a block
+    n_new = np.minimum(n_new, sl)
+    qsl = np.concatenate([[0], np.cumsum(n_new)]).astype(np.int32)
+    q = q[:qsl[-1]]
+    qb = O.encode(q, O.BF16)
+    if kv_kind == O.FP8_E4M3:
+        kb, vb = O.encode(k / 4, kv_kind), O.encode(v / 4, kv_kind)
+        ks = vs = 4.0
+        nan_bits = 0x7F
+    else:
+        kb, vb = O.encode(k, kv_kind), O.encode(v, kv_kind)
+        ks = vs = 1.0
+        nan_bits = 0x7FC0
+    ref = O.paged_attention_prefill(qb, O.BF16, kb, vb, kv_kind, bt, sl, qsl, 0.088, ks, vs, precision=1)
+    for s in range(nseq):
+        last = bt[s, (sl[s] - 1) // 16]
+        kb[last, :, :, sl[s] % 16:] = nan_bits
+        vb[last, :, :, sl[s] % 16:] = nan_bits
+    got = run_prefill(dev, qb, O.BF16, kb, vb, kv_kind, bt, sl, qsl, 0.088, ks, vs,
+                      label=f"nan-tail nseq={nseq}")
+    assert_close(got, ref, TOL_FP8 if kv_kind == O.FP8_E4M3 else TOL_BF16, f"prefill nan tail nseq={nseq}")
+
+
 def test_prefill_single_token_sequences_equal_decode(dev):
     rng = np.random.default_rng(9)
     q, k, v, bt, sl, qsl = make_case(rng, [1] * 6, [0, 15, 16, 100, 257, 31], 32, 8, 128)
