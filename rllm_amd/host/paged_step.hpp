@@ -12,10 +12,14 @@
 //     sequences with one token each), computes the slot of every token
 //     (compute_slot_mappings, model_runner.rs:806-826), splits the prefill
 //     and decode groups into their own flattened tables, packs everything
-//     into one pinned staging buffer and issues ONE host-to-device copy on the
-//     step's stream.  Staging is double-buffered behind events, so the next
-//     step can be prepared while this one's copy is in flight; the device
-//     buffer is reused in stream order.
+//     into one pinned staging buffer and moves it to the device with ONE copy
+//     kernel on the step's stream.  The kernel reads the pinned buffer
+//     through its device mapping, so the step's kernels follow it on the same
+//     compute queue; a DMA-engine copy would put an engine-to-queue hand-off
+//     (tens of microseconds) in front of every step.  Staging is
+//     double-buffered behind events, so the next step can be prepared while
+//     this one's copy is in flight; the device buffer is reused in stream
+//     order.
 //   * paged_attention_step writes the step's k / v into the cache (optionally
 //     with the fused rotary embedding), then runs chunked prefill over the
 //     prefill tokens and decode over the decode tokens, all on one stream,
@@ -49,16 +53,14 @@ public:
             void* p = nullptr;
             if (hipHostMalloc(&p, m.capacity_, hipHostMallocDefault) != hipSuccess) return fail(m);
             m.staging_[i] = static_cast<uint8_t*>(p);
+            void* dp = nullptr;   // the same pages as the copy kernel sees them
+            if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess || dp == nullptr) return fail(m);
+            m.staging_dev_[i] = static_cast<const uint8_t*>(dp);
             if (hipEventCreateWithFlags(&m.copied_[i], hipEventDisableTiming) != hipSuccess) return fail(m);
         }
         void* d = nullptr;
         if (hipMalloc(&d, m.capacity_) != hipSuccess) return fail(m);
         m.device_ = static_cast<uint8_t*>(d);
-        // a second stream (default priority) on which paged_attention_step
-        // runs the prefill group beside the decode group
-        if (hipStreamCreateWithFlags(&m.side_, hipStreamNonBlocking) != hipSuccess) return fail(m);
-        if (hipEventCreateWithFlags(&m.fork_, hipEventDisableTiming) != hipSuccess) return fail(m);
-        if (hipEventCreateWithFlags(&m.join_, hipEventDisableTiming) != hipSuccess) return fail(m);
         return Result<DeviceStepMetadata>::ok(std::move(m));
     }
 
@@ -71,18 +73,14 @@ public:
             release();
             for (int i = 0; i < 2; ++i) {
                 staging_[i] = o.staging_[i];
+                staging_dev_[i] = o.staging_dev_[i];
                 copied_[i] = o.copied_[i];
                 o.staging_[i] = nullptr;
+                o.staging_dev_[i] = nullptr;
                 o.copied_[i] = nullptr;
             }
             device_ = o.device_;
             o.device_ = nullptr;
-            side_ = o.side_;
-            fork_ = o.fork_;
-            join_ = o.join_;
-            o.side_ = nullptr;
-            o.fork_ = nullptr;
-            o.join_ = nullptr;
             capacity_ = o.capacity_;
             next_ = o.next_;
             num_tokens = o.num_tokens;
@@ -128,7 +126,7 @@ public:
     }
 
     // Builds the step's metadata (check_step first, and the capacity) and
-    // uploads it with one copy on `stream`.
+    // uploads it with one copy kernel on `stream`.
     Result<void> upload(const StepInput& in, size_t block_size, size_t num_blocks, hipStream_t stream) {
         const Result<void> ok = check_step(in, block_size, num_blocks);
         if (ok.is_err()) return ok;
@@ -187,8 +185,10 @@ public:
             fill_row(dbt + s * md, in.block_tables[np + s], md);
             dsl[s] = static_cast<int32_t>(in.seq_lens[np + s]);
         }
-        if (const hipError_t e = hipMemcpyAsync(device_, h, need, hipMemcpyHostToDevice, stream); e != hipSuccess)
-            return hip_err(e);
+        if (const int32_t rc = rllm_block_copy(staging_dev_[buf], device_, static_cast<int64_t>(need),
+                                               reinterpret_cast<uintptr_t>(stream));
+            rc != 0)
+            return check(rc);
         if (const hipError_t e = hipEventRecord(copied_[buf], stream); e != hipSuccess) return hip_err(e);
 
         num_tokens = static_cast<int64_t>(tokens);
@@ -254,32 +254,18 @@ private:
             if (staging_[i]) (void)hipHostFree(staging_[i]);
             copied_[i] = nullptr;
             staging_[i] = nullptr;
+            staging_dev_[i] = nullptr;
         }
-        if (side_) {
-            (void)hipStreamSynchronize(side_);
-            (void)hipStreamDestroy(side_);
-        }
-        if (fork_) (void)hipEventDestroy(fork_);
-        if (join_) (void)hipEventDestroy(join_);
-        side_ = nullptr;
-        fork_ = join_ = nullptr;
         if (device_) (void)hipFree(device_);
         device_ = nullptr;
     }
 
     uint8_t* staging_[2] = {nullptr, nullptr};
+    const uint8_t* staging_dev_[2] = {nullptr, nullptr};
     hipEvent_t copied_[2] = {nullptr, nullptr};
     uint8_t* device_ = nullptr;
     size_t capacity_ = 0;
     int next_ = 0;
-    hipStream_t side_ = nullptr;
-    hipEvent_t fork_ = nullptr, join_ = nullptr;
-
-public:
-    // the side stream and the fork / join events of paged_attention_step
-    hipStream_t side_stream() const { return side_; }
-    hipEvent_t fork_event() const { return fork_; }
-    hipEvent_t join_event() const { return join_; }
 };
 
 // Rotary embedding inputs for paged_attention_step (device tables from
@@ -338,32 +324,16 @@ inline Result<void> paged_attention_step(const DeviceStepMetadata& m, void* out,
     const float scale = p.scale;
     const bool fp8 = kv == DType::FP8E4M3 || kv == DType::FP8E5M2;
     const float ks = fp8 ? k_scale : 1.0f, vs = fp8 ? v_scale : 1.0f;
-    // 2. prefill group.  With decode work too, it runs on the side stream,
-    // forked after the cache write and joined before the call returns, so a
-    // small prefill chunk (few workgroups) shares the GPU with the decode
-    // group instead of running alone.  The two write disjoint rows of out.
-    const bool fork = m.num_prefill_seqs > 0 && m.num_decode_seqs > 0 && m.side_stream() != nullptr;
+    // 2. prefill group, on the same stream as the decode group that follows.
+    // The decode grid holds one 512-register wave per SIMD, so a prefill
+    // workgroup (eight waves) cannot run beside it: on a second stream the
+    // prefill only fills in as decode waves retire, which measured slower
+    // than running the two groups in series.
     if (m.num_prefill_seqs > 0) {
-        uintptr_t pst = st;
-        if (fork) {
-            if (const hipError_t e = hipEventRecord(m.fork_event(), stream); e != hipSuccess)
-                return check(static_cast<int32_t>(e));
-            if (const hipError_t e = hipStreamWaitEvent(m.side_stream(), m.fork_event(), 0); e != hipSuccess)
-                return check(static_cast<int32_t>(e));
-            pst = reinterpret_cast<uintptr_t>(m.side_stream());
-        }
         const Result<void> r = check(rllm_paged_attention_prefill_ex(
             out, q, key_cache, value_cache, m.prefill_block_tables, m.prefill_seq_lens, m.prefill_query_start_loc,
-            m.num_prefill_seqs, m.num_prefill_tokens, hq, hkv, d, bs, m.prefill_max_blocks, scale, a, c, ks, vs, pst));
-        if (fork) {
-            // recorded even after an error: `stream` joins it below in every case
-            if (const hipError_t e = hipEventRecord(m.join_event(), m.side_stream()); e != hipSuccess)
-                return check(static_cast<int32_t>(e));
-        }
-        if (r.is_err()) {
-            if (fork) (void)hipStreamWaitEvent(stream, m.join_event(), 0);
-            return r;
-        }
+            m.num_prefill_seqs, m.num_prefill_tokens, hq, hkv, d, bs, m.prefill_max_blocks, scale, a, c, ks, vs, st));
+        if (r.is_err()) return r;
     }
     // 3. decode group: its tokens follow the prefill tokens
     if (m.num_decode_seqs > 0) {
@@ -374,11 +344,6 @@ inline Result<void> paged_attention_step(const DeviceStepMetadata& m, void* out,
             static_cast<uint8_t*>(out) + off, static_cast<const uint8_t*>(q) + off, key_cache, value_cache,
             m.decode_block_tables, m.decode_seq_lens, m.num_decode_seqs, hq, hkv, d, bs, m.decode_max_blocks, scale,
             a, c, ks, vs, 0, nullptr, 0, st));
-        // join: later work on `stream` (the next step's metadata upload
-        // included) waits for the prefill group
-        if (fork)
-            if (const hipError_t e = hipStreamWaitEvent(stream, m.join_event(), 0); e != hipSuccess && r.is_ok())
-                return check(static_cast<int32_t>(e));
         if (r.is_err()) return r;
     }
     return Result<void>::ok();
