@@ -340,3 +340,19 @@ def test_prefill_split_leaves_rows_past_the_batch_untouched(dev):
     got = f32(out)
     assert np.all(got[T:] == 7.0), "rows past query_start_loc[num_seqs] were written"
     assert_close(got[:T], ref, TOL_BF16, "rows of the batch")
+
+
+def test_prefill_kv_split_merge_is_deterministic(dev):
+    """The merge sums every row's splits in split order, so repeated calls on
+    the reused per-stream workspace give the same bits."""
+    rng = np.random.default_rng(91)
+    hq, hkv, D = 32, 8, 128
+    q, k, v, bt, sl, qsl = make_case(rng, [512], [2048], hq, hkv, D)
+    qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
+    scale = 1 / np.sqrt(D)
+    ref = O.paged_attention_prefill(qb, O.BF16, kb, vb, O.BF16, bt, sl, qsl, scale, precision=1)
+    runs = [run_prefill(dev, qb, O.BF16, kb, vb, O.BF16, bt, sl, qsl, scale, 1.0, 1.0,
+                        label=f"kv split determinism run {i}") for i in range(4)]
+    assert_close(runs[0], ref, TOL_BF16, "kv split determinism vs oracle")
+    for i in range(1, 4):
+        assert np.array_equal(runs[i], runs[0]), f"run {i} differs from run 0"
