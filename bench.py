@@ -772,9 +772,24 @@ def bench_decode(args, w, lib, dev, cpu=True, device_values=False, calibrate=Tru
     fn = lib.rllm_paged_attention_decode_ex
     qp, op, btp, slp = q.data_ptr(), out.data_ptr(), bt.data_ptr(), sl.data_ptr()
     pool_ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in pools]
+    prefix_blocks = 0
+    if getattr(args, "cascade", False):
+        # the shared prefix as the host metadata finds it (attention.rs:204-226),
+        # kept to blocks every context covers in full
+        from rllm_amd.attention import AttentionMetadata
+        meta = AttentionMetadata.for_decode(w.seq_lens.tolist(), w.block_tables.tolist(), w.max_blocks)
+        meta.detect_common_prefix_blocks()
+        prefix_blocks = min(meta.common_prefix_blocks, int(w.seq_lens.min()) // w.block_size)
 
     def step(i):
         kp, vp = pool_ptrs[i % len(pool_ptrs)]
+        if prefix_blocks:
+            rc = lib.rllm_paged_attention_decode_prefix_ex(
+                op, qp, kp, vp, btp, slp, w.num_seqs, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size,
+                w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, kv_code, k_scale, v_scale, prefix_blocks, sh)
+            if rc:
+                raise rllm_amd.KernelError(rc, "rllm_paged_attention_decode_prefix_ex")
+            return
         rc = fn(op, qp, kp, vp, btp, slp, w.num_seqs, w.num_q_heads, w.num_kv_heads, w.head_dim,
                 w.block_size, w.max_blocks, w.scale, rllm_amd.DTYPE_BF16, kv_code, k_scale, v_scale,
                 args.partition, None, 0, sh)
@@ -825,12 +840,13 @@ def bench_decode(args, w, lib, dev, cpu=True, device_values=False, calibrate=Tru
                    "sum_context_tokens": int(w.seq_lens.sum()),
                    "max_context": int(w.seq_lens.max()), "partition": args.partition,
                    "kv_pools": "one (warm cache)" if args.warm_cache else f"{len(pools)} rotated",
+                   "cascade_prefix_blocks": prefix_blocks,
                    "parallelism": f"tp{args.tp} share on one GPU" if args.tp > 1 else "single GPU"},
         "seqs_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(w.name),
+                     "traffic": None if prefix_blocks else measured_traffic(w.name),
                      "kernel_ms": round(kernel_ms, 5),
                      "per_launch_ms_p10_p50_p90": [round(float(np.percentile(call_ms, q)), 5) for q in (10, 50, 90)],
                      "algorithmic_bytes": nbytes},
@@ -877,6 +893,9 @@ def main() -> int:
     ap.add_argument("--prefill-seqs", type=int, default=0,
                     help="config 5: time only the first N sequences' chunks (1: one prompt, the small-batch "
                          "path that splits the KV range)")
+    ap.add_argument("--cascade", action="store_true",
+                    help="decode through rllm_paged_attention_decode_prefix_ex with the tables' common prefix "
+                         "(config 4: 64 blocks shared by all 128 sequences)")
     ap.add_argument("--warm-cache", action="store_true",
                     help="decode: every step reads the same KV pool (L2/MALL keep what fits; config 4a's "
                          "shared prefix) instead of rotating over pools that do not fit the 256 MB MALL")

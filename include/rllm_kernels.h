@@ -152,6 +152,36 @@ int32_t rllm_paged_attention_decode_ex(void *output, const void *query, const vo
                                        float v_scale, int64_t partition_size, void *workspace,
                                        int64_t workspace_bytes, uintptr_t stream);
 
+/* New: decode of a batch whose block tables share a prefix, the cascade
+ * form of rllm_paged_attention_decode_ex for the shared prefixes that
+ * AttentionMetadata::detect_common_prefix_blocks (attention.rs:204-226)
+ * finds.  The reference has the detection but no kernel that uses it.
+ *   num_prefix_blocks  the first num_prefix_blocks entries of every table
+ *             are the same physical blocks, and every sequence's context
+ *             covers them (seq_lens[s] >= num_prefix_blocks * block_size).
+ *             A shorter context is still attended correctly, but the prefix
+ *             block's slots past every sequence's context must then hold
+ *             finite values.  0 runs the plain decode.
+ * The prefix's keys and values are read once per kv head for the whole
+ * batch, with matrix cores; each sequence's blocks past the prefix are
+ * attended separately, and a reduction merges the two in the log-sum-exp
+ * domain.  The result equals rllm_paged_attention_decode_ex's within
+ * rounding.  Shapes outside the tuned set (head_dim 64 / 128, block size 16,
+ * GQA 1 / 2 / 4 / 8), and f16 queries whose scale * log2(e) (* k_scale)
+ * exceeds 1, run the plain decode.  Scratch is library-owned per (device,
+ * stream); calls on one stream must not be captured unless an eager call of
+ * the same or a larger shape ran on that stream before (a capture with too
+ * small a buffer runs the plain decode instead). */
+int32_t rllm_paged_attention_decode_prefix_ex(void *output, const void *query, const void *key_cache,
+                                              const void *value_cache, const int32_t *block_tables,
+                                              const int32_t *seq_lens, int64_t num_seqs,
+                                              int64_t num_q_heads, int64_t num_kv_heads,
+                                              int64_t head_dim, int64_t block_size,
+                                              int64_t max_num_blocks_per_seq, float scale,
+                                              int32_t q_dtype, int32_t kv_dtype, float k_scale,
+                                              float v_scale, int64_t num_prefix_blocks,
+                                              uintptr_t stream);
+
 /* New: bytes of split-K workspace rllm_paged_attention_decode_ex needs for
  * these shapes on the current device (0 when nothing is split); negative on
  * invalid arguments. */

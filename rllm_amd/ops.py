@@ -104,6 +104,37 @@ def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     return out
 
 
+def paged_decode_prefix(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        block_tables: torch.Tensor, seq_lens: torch.Tensor, scale: float,
+                        num_prefix_blocks: int, *, kv_dtype: Optional[int] = None, k_scale: float = 1.0,
+                        v_scale: float = 1.0, out: Optional[torch.Tensor] = None, validate: bool = True,
+                        stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """Decode of a batch whose tables share their first num_prefix_blocks
+    entries, through rllm_paged_attention_decode_prefix_ex (the prefix is
+    attended once for the batch, then merged with each sequence's rest)."""
+    B, hq, d = q.shape
+    _check_common(q, k_cache, v_cache, block_tables, seq_lens, B)
+    nb, hkv, d2, bs = k_cache.shape
+    kv = _kv_code(k_cache, kv_dtype)
+    qd = _TORCH_16[q.dtype]
+    if kv in (DTYPE_F16, DTYPE_BF16) and kv != qd:
+        raise TypeError("a 16-bit cache must have the dtype of q")
+    if validate:
+        validate_tables(block_tables, seq_lens, nb, bs)
+        if num_prefix_blocks:
+            bt = block_tables.cpu()
+            if not bool((bt[:, :num_prefix_blocks] == bt[:1, :num_prefix_blocks]).all()):
+                raise ValueError("the tables do not share their first num_prefix_blocks entries")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous() or out.device != q.device:
+        raise ValueError("out must be a contiguous tensor like q")
+    call("rllm_paged_attention_decode_prefix_ex", _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache),
+         _ptr(block_tables), _ptr(seq_lens), B, hq, hkv, d, bs, block_tables.shape[1], scale,
+         qd, kv, k_scale, v_scale, num_prefix_blocks, _stream(stream))
+    return out
+
+
 def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                   block_tables: torch.Tensor, seq_lens: torch.Tensor,
                   query_start_loc: torch.Tensor, scale: float, *, kv_dtype: Optional[int] = None,
