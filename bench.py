@@ -47,8 +47,10 @@ PROFILES = os.path.join(ROOT, "profiles")
 # the sources whose kernels a traffic summary measured: a summary counts only
 # while their digest matches the one recorded with it
 KERNEL_SOURCES = {
-    "decode": ["rllm_amd/csrc/paged_attention_decode.hip", "rllm_amd/csrc/common.h"],
-    "prefill": ["rllm_amd/csrc/paged_attention_prefill.hip", "rllm_amd/csrc/common.h"],
+    "decode": ["rllm_amd/csrc/paged_attention_decode.hip", "rllm_amd/csrc/prefill_kernel.h",
+               "rllm_amd/csrc/common.h"],
+    "prefill": ["rllm_amd/csrc/paged_attention_prefill.hip", "rllm_amd/csrc/prefill_kernel.h",
+                "rllm_amd/csrc/common.h"],
 }
 
 

@@ -2,7 +2,10 @@
 // the cascade decode over a shared prefix (rllm_paged_attention_decode_prefix_ex):
 // the prefill kernel's prefix mode computes every decode row's attention over
 // the prefix blocks, as partials the decode reduction merges with those of
-// the per-sequence suffixes.
+// the per-sequence suffixes.  With 16-bit caches the decode translation unit
+// runs that mode itself (cascade_kernel, through prefill_kernel.h) and uses
+// only the split count from here; FP8 caches launch the partials through
+// launch_prefix_partials.
 #pragma once
 
 #include <hip/hip_runtime.h>

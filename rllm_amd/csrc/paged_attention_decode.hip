@@ -40,6 +40,7 @@
 #include "generic_attention.h"
 #include "workspace.h"
 #include "cascade.h"
+#include "prefill_kernel.h"
 #include "../../include/rllm_kernels.h"
 
 #include <algorithm>
@@ -727,12 +728,12 @@ struct Attn {
 // ---------------------------------------------------------------------------
 // Partitioned decode: one wave per (sequence, kv head, context partition).
 // ---------------------------------------------------------------------------
+// The body for item `bid` of the grid, one wave: decode_kernel runs it for its
+// workgroup index, the cascade kernel for each wave of its suffix workgroups.
 template <int QKIND, int KVKIND, int D, int G>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_part_body(const DecodeArgs& a, typename Attn<QKIND, KVKIND, D, G>::QP& qp,
+                                                 typename Attn<QKIND, KVKIND, D, G>::PL& pl, int bid) {
     using A = Attn<QKIND, KVKIND, D, G>;
-    __shared__ __align__(16) typename A::QP qp;
-    __shared__ __align__(16) typename A::PL pl;
-    int bid = blockIdx.x;
     const int grid_parts = a.max_parts - a.part_offset;   // the grid's partitions per (sequence, kv head)
     const int part = bid % grid_parts;
     bid /= grid_parts;
@@ -767,6 +768,51 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void de
             }
         },
         [] {});
+}
+
+template <int QKIND, int KVKIND, int D, int G>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
+    using A = Attn<QKIND, KVKIND, D, G>;
+    __shared__ __align__(16) typename A::QP qp;
+    __shared__ __align__(16) typename A::PL pl;
+    decode_part_body<QKIND, KVKIND, D, G>(a, qp, pl, static_cast<int>(blockIdx.x));
+}
+
+// ---------------------------------------------------------------------------
+// Cascade decode over a shared prefix, one launch for both kinds of work:
+// workgroups [0, prefix_wgs) run the prefill kernel's shared-prefix mode (the
+// prefix partials of every row, latency-bound: ~15 us of fixed costs for a
+// few tiles); the others run the partitioned decode over the blocks past the
+// prefix, `dpw` waves each, one (sequence, kv head, partition) item a wave
+// (bandwidth-bound).  Both write partials for decode_reduce_kernel.  In one
+// launch the two overlap on the GPU, which two launches on one stream cannot
+// do and two streams do only at the price of their fork and join events.
+// Workgroups of PP_THREADS threads (the prefill body needs its 8 waves);
+// waves past dpw leave at once.  The suffix waves keep their q and weights in
+// the LDS the prefill body uses for its tiles.
+// ---------------------------------------------------------------------------
+template <int QKIND, int KVKIND, int D, int G>
+__global__ __launch_bounds__(PP_THREADS, 1) void cascade_kernel(PrefillArgs pa, const int32_t* __restrict__ block_tables,
+                                                                DecodeArgs da, int32_t prefix_wgs, int32_t items,
+                                                                int32_t dpw) {
+    using A = Attn<QKIND, KVKIND, D, G>;
+    using QP = typename A::QP;
+    using PL = typename A::PL;
+    constexpr int NW = PP_THREADS / 64;
+    static_assert(sizeof(QP) % 16 == 0 && sizeof(PL) % 16 == 0, "16-byte aligned per-wave state");
+    constexpr int WORDS = std::max<int>(pf_lds_words<D>(), NW * static_cast<int>(sizeof(QP) + sizeof(PL)) / 16);
+    __shared__ uint4 lds[WORDS];
+    const int b = static_cast<int>(blockIdx.x);
+    if (b < prefix_wgs) {
+        prefill_body<QKIND, KVKIND, D, G>(pa, block_tables, b, lds);
+        return;
+    }
+    const int wid = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int item = (b - prefix_wgs) * dpw + wid;
+    if (wid >= dpw || item >= items) return;
+    QP* const qp_all = reinterpret_cast<QP*>(lds);
+    PL* const pl_all = reinterpret_cast<PL*>(lds + NW * sizeof(QP) / 16);
+    decode_part_body<QKIND, KVKIND, D, G>(da, qp_all[wid], pl_all[wid], item);
 }
 
 // Merges the partitions of every (sequence, q head) that has more than one.
@@ -1366,6 +1412,7 @@ struct Kernels {
     const void* stream4;   // STREAM_WPB_WIDE waves per workgroup
     const void* stream4_small;   // same with SMALL_SHARE_PF_V V blocks in flight (null if none)
     const void* reduce;
+    const void* cascade;   // cascade_kernel (16-bit caches; null for FP8)
 };
 
 // V blocks in flight of the small-share stream kernel: a launch of at least
@@ -1382,14 +1429,17 @@ constexpr int64_t SMALL_SHARE_BLOCKS = 32;
 template <int QKIND, int KVKIND, int D, int G>
 Kernels kernels_of() {
     const void* small = nullptr;
+    const void* cascade = nullptr;
     if constexpr (KVKIND == QKIND && G <= 4)
         small = reinterpret_cast<const void*>(
             &decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB_WIDE, SMALL_SHARE_PF_V>);
+    if constexpr (KVKIND == QKIND) cascade = reinterpret_cast<const void*>(&cascade_kernel<QKIND, KVKIND, D, G>);
     return {reinterpret_cast<const void*>(&decode_kernel<QKIND, KVKIND, D, G>),
             reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, 1>),
             reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB_WIDE>),
             small,
-            reinterpret_cast<const void*>(&decode_reduce_kernel<QKIND, D>)};
+            reinterpret_cast<const void*>(&decode_reduce_kernel<QKIND, D>),
+            cascade};
 }
 
 template <int QKIND, int KVKIND, int D>
@@ -1552,14 +1602,24 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
 
 // Cascade decode over a shared prefix: the first prefix_blocks entries of
 // every table are the same physical blocks.  The prefix is attended once for
-// the whole batch by the MFMA prefill kernel (the decode queries as the
-// tokens of one virtual sequence), which writes each row's partial in the
-// first slots; the partitioned decode kernel attends every sequence's blocks
-// past the prefix into the next slots; the reduction merges them.  The
-// prefix's K and V are then read once per kv head instead of once per
-// sequence.  Shapes or scalings the MFMA kernel does not take run the plain
-// decode.
+// the whole batch by the MFMA prefill kernel's shared-prefix mode (the decode
+// queries as the tokens of one virtual sequence), which writes each row's
+// partial in the first slots; the partitioned decode attends every
+// sequence's blocks past the prefix into the next slots; the reduction
+// merges them.  The prefix's K and V are then read once per kv head instead
+// of once per sequence.  With 16-bit caches both run in one cascade_kernel
+// launch; FP8 caches launch them in series.  Shapes or scalings the MFMA
+// kernel does not take run the plain decode.
 constexpr int64_t CASCADE_MAX_SUFFIX_PARTS = 8;   // suffix partitions per row, at most
+
+// Waves per suffix workgroup of cascade_kernel: the suffix items spread over
+// the CUs the prefix workgroups leave free, at most 8 a workgroup.  Config
+// 4a (64 prefix workgroups, 1024 items on 256 CUs): 6 waves measured 38.9
+// against 43.9 us with 8 (two waves on every SIMD of half the CUs).
+int32_t cascade_waves_per_wg(int64_t items, int64_t prefix_wgs) {
+    const int64_t free_cus = std::max<int64_t>(1, int64_t(device_cus()) - prefix_wgs);
+    return static_cast<int32_t>(std::min<int64_t>(PP_THREADS / 64, std::max<int64_t>(1, (items + free_cus - 1) / free_cus)));
+}
 
 int32_t decode_prefix_impl(void* out, const void* q, const void* kc, const void* vc, const int32_t* bt,
                            const int32_t* seq_lens, int64_t num_seqs, int64_t hq, int64_t hkv, int64_t d,
@@ -1601,12 +1661,6 @@ int32_t decode_prefix_impl(void* out, const void* q, const void* kc, const void*
     float* part_out = static_cast<float*>(ws);
     float* part_ml = part_out + rows * max_parts * d;
     hipStream_t st = as_stream(stream);
-    // in series on `stream`: running the prefix partials on a second stream
-    // beside the suffix decode measured slower (config 4a 51.7 -> 59.9 us;
-    // the fork and join events cost 6 and 12 us)
-    rc = launch_prefix_partials(q, kc, vc, bt, seq_lens, num_seqs, hq, hkv, d, prefix_blocks, scale, q_dtype,
-                                kv_dtype, k_scale, v_scale, S, part_out, part_ml, max_parts, st);
-    if (rc) return rc;
     DecodeArgs a{};
     a.out = out;
     a.q = static_cast<const uint16_t*>(q);
@@ -1627,8 +1681,29 @@ int32_t decode_prefix_impl(void* out, const void* q, const void* kc, const void*
     a.max_parts = static_cast<int32_t>(max_parts);
     a.block_offset = static_cast<int32_t>(prefix_blocks);
     a.part_offset = static_cast<int32_t>(S);
-    rc = launch(kern.part, dim3(static_cast<unsigned>(num_seqs * hkv * suffix_parts)), a, st);
-    if (rc) return rc;
+    const int64_t items = num_seqs * hkv * suffix_parts;
+    if (kern.cascade) {
+        // one launch: the prefix workgroups first, then the suffix waves
+        const int64_t pw = prefix_base_wgs(num_seqs, hq, hkv) * S;
+        int32_t dpw = cascade_waves_per_wg(items, pw);
+        const int64_t grid = pw + (items + dpw - 1) / dpw;
+        RLLM_CHECK_ARG(grid <= INT32_MAX);
+        PrefillArgs pa = prefix_mode_args(q, kc, vc, bt, seq_lens, num_seqs, hq, hkv, prefix_blocks, scale,
+                                          kv_dtype, k_scale, v_scale, S, part_out, part_ml, max_parts);
+        const int32_t* bt_arg = bt;
+        int32_t pw32 = static_cast<int32_t>(pw), items32 = static_cast<int32_t>(items);
+        void* args[] = {&pa, const_cast<int32_t**>(&bt_arg), &a, &pw32, &items32, &dpw};
+        RLLM_TRY(hipLaunchKernel(kern.cascade, dim3(static_cast<unsigned>(grid)), dim3(PP_THREADS), args, 0, st));
+    } else {
+        // FP8 caches, in series on `stream`: running the prefix partials on a
+        // second stream beside the suffix decode measured slower (config 4a
+        // 51.7 -> 59.9 us; the fork and join events cost 6 and 12 us)
+        rc = launch_prefix_partials(q, kc, vc, bt, seq_lens, num_seqs, hq, hkv, d, prefix_blocks, scale, q_dtype,
+                                    kv_dtype, k_scale, v_scale, S, part_out, part_ml, max_parts, st);
+        if (rc) return rc;
+        rc = launch(kern.part, dim3(static_cast<unsigned>(items)), a, st);
+        if (rc) return rc;
+    }
     return launch(kern.reduce, dim3(static_cast<unsigned>(rows)), a, st);
 }
 

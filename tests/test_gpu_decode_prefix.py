@@ -149,6 +149,25 @@ def test_prefix_config4a_full_vs_oracle_and_plain_decode(dev):
     print(f"config 4a cascade: rel_l2 {rl2:.3e}")
 
 
+@pytest.mark.parametrize("B,hq,hkv,D,P,suffix", [
+    (3, 4, 1, 128, 7, (1, 40)),         # three suffix waves: one wave per suffix workgroup
+    (251, 6, 3, 64, 8, (0, 40)),        # several waves per workgroup, the last one partly filled
+    (24, 8, 2, 128, 8, (2000, 4000)),   # eight suffix partitions per row
+    (2100, 32, 8, 64, 4, (0, 16)),      # the prefix workgroups alone fill the GPU (unsplit prefix)
+], ids=["one-wave", "partial-tail", "eight-partitions", "prefix-fills-gpu"])
+def test_prefix_single_launch_grids_vs_oracle(dev, B, hq, hkv, D, P, suffix):
+    """With 16-bit caches the prefix workgroups and the suffix waves share one
+    launch, whose suffix workgroups carry 1 to 8 waves (the suffix items over
+    the CUs the prefix leaves free).  Grids of each kind, against the oracle."""
+    rng = np.random.default_rng(1200 + B + D)
+    q, k, v, bt, sl = prefix_case(rng, B, hq, hkv, D, P, suffix)
+    qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
+    scale = 1 / np.sqrt(D)
+    ref = oracle_ref(qb, O.BF16, kb, vb, O.BF16, bt, sl, scale)
+    got = run_prefix(dev, qb, O.BF16, kb, vb, O.BF16, bt, sl, scale, P, label=f"grid B={B}")
+    assert_close(got, ref, TOL_BF16, f"prefix grid B={B} Hq={hq} Hkv={hkv} D={D}")
+
+
 def test_prefix_repeated_calls_give_the_same_bits(dev):
     rng = np.random.default_rng(909)
     q, k, v, bt, sl = prefix_case(rng, 33, 32, 8, 128, 12, (1, 600))
