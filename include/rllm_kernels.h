@@ -182,6 +182,33 @@ int32_t rllm_paged_attention_decode_prefix_ex(void *output, const void *query, c
                                               float v_scale, int64_t num_prefix_blocks,
                                               uintptr_t stream);
 
+/* New: one step's attention over a mixed batch, in place of the pair of
+ * calls the reference's ModelRunner::run_paged_attention makes "depending on
+ * the batch composition" (model_runner.rs:404-414): the prefill group is
+ * rllm_paged_attention_prefill_ex's arguments (prefill_*), the decode group
+ * rllm_paged_attention_decode_ex's with partition_size 0 and no workspace
+ * (decode_*), over the same caches, heads and scales.  The two groups'
+ * outputs and queries are separate arrays (they may be two row ranges of one
+ * buffer).  With 16-bit caches, the tuned shapes and a prefill group of at
+ * most half as many workgroups as the GPU has CUs (256 query rows a
+ * workgroup: 64 tokens at GQA 4), both groups run in one kernel launch, the
+ * prefill on its own CUs beside the decode; otherwise, or when either group is
+ * empty, the two entry points run in series.  Results equal the two entry
+ * points' within rounding (the prefill group is never split over its KV
+ * range here).  Scratch is the decode's library-owned stream workspace, per
+ * (device, stream); a capture on a stream without it runs in series. */
+int32_t rllm_paged_attention_mixed_ex(void *prefill_output, const void *prefill_query,
+                                      const int32_t *prefill_block_tables, const int32_t *prefill_seq_lens,
+                                      const int32_t *prefill_query_start_loc, int64_t prefill_num_seqs,
+                                      int64_t prefill_num_tokens, int64_t prefill_max_blocks,
+                                      void *decode_output, const void *decode_query,
+                                      const int32_t *decode_block_tables, const int32_t *decode_seq_lens,
+                                      int64_t decode_num_seqs, int64_t decode_max_blocks,
+                                      const void *key_cache, const void *value_cache,
+                                      int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                      int64_t block_size, float scale, int32_t q_dtype, int32_t kv_dtype,
+                                      float k_scale, float v_scale, uintptr_t stream);
+
 /* New: bytes of split-K workspace rllm_paged_attention_decode_ex needs for
  * these shapes on the current device (0 when nothing is split); negative on
  * invalid arguments. */

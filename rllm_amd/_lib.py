@@ -52,6 +52,8 @@ SIGNATURES = {
                                        _I32, _I32, _F, _F, _I64, _P, _I64, _U],
     "rllm_paged_attention_decode_prefix_ex": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F,
                                               _I32, _I32, _F, _F, _I64, _U],
+    "rllm_paged_attention_mixed_ex": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P,
+                                      _I64, _I64, _I64, _I64, _F, _I32, _I32, _F, _F, _U],
     "rllm_paged_attention_decode_noalloc": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F,
                                             _I32, _I32, _F, _F, _I64, _U],
     "rllm_paged_attention_decode_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64, _I64],

@@ -142,33 +142,16 @@ int32_t prefill_impl(void* out, const void* q, const void* kc, const void* vc, c
         return generic_attention(out, q, kc, vc, bt, seq_lens, qsl, num_seqs, num_tokens, hq, hkv, d, bs, maxb,
                                  scale, q_dtype, kv_dtype, k_scale, v_scale, as_stream(stream));
 
-    PrefillArgs a{};
-    a.out = out;
-    a.q = static_cast<const uint16_t*>(q);
-    a.k_cache = kc;
-    a.v_cache = vc;
-    a.block_tables = bt;
-    a.seq_lens = seq_lens;
-    a.query_start_loc = qsl;
-    a.num_seqs = static_cast<int32_t>(num_seqs);
-    a.num_q_heads = static_cast<int32_t>(hq);
-    a.num_kv_heads = static_cast<int32_t>(hkv);
-    a.max_blocks = static_cast<int32_t>(maxb);
-    const bool fp8 = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
-    a.s_scale = scale * PF_LOG2E * (fp8 ? k_scale : 1.f);
-    a.v_scale = fp8 ? v_scale : 1.f;
-    // the kernel multiplies the queries by s_scale in the q type: f16 queries
-    // could overflow when it exceeds 1 (bf16 has the float range); that rare
-    // case runs on the shape-general kernel, which scales the fp32 scores
-    if (q_dtype == KIND_F16 && !(std::fabs(a.s_scale) <= 1.f))
+    // f16 queries whose pre-scale could overflow: the shape-general kernel,
+    // which scales the fp32 scores
+    if (!q_prescale_ok(q_dtype, kv_dtype, scale, k_scale))
         return generic_attention(out, q, kc, vc, bt, seq_lens, qsl, num_seqs, num_tokens, hq, hkv, d, bs, maxb,
                                  scale, q_dtype, kv_dtype, k_scale, v_scale, as_stream(stream));
 
-    // an upper bound of the query tiles: sum_s ceil(n_s/QT) <= T/QT + num_seqs
-    const int64_t QT = PP_ROWS / G;
-    const int64_t tiles = (num_tokens + QT - 1) / QT + num_seqs;
-    const int64_t nwg = tiles * hkv;
+    const int64_t nwg = chunk_base_wgs(num_tokens, num_seqs, hq, hkv);
     RLLM_CHECK_ARG(nwg <= INT32_MAX);
+    PrefillArgs a = chunk_mode_args(out, q, kc, vc, bt, seq_lens, qsl, num_seqs, hq, hkv, maxb, scale, kv_dtype,
+                                    k_scale, v_scale, nwg);
     // few workgroups (a small batch): split every row's KV range over up to
     // 8 workgroups and merge the partials in a second kernel
     const int64_t splits = prefill_splits(nwg, maxb);
@@ -250,11 +233,7 @@ int64_t prefix_partial_splits(int64_t num_seqs, int64_t hq, int64_t hkv, int64_t
 
 bool prefix_partials_supported(int64_t hq, int64_t hkv, int64_t d, int64_t bs, int32_t q_dtype, int32_t kv_dtype,
                                float scale, float k_scale) {
-    if (!specialised_shape(hq, hkv, d, bs)) return false;
-    const bool fp8 = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
-    const float s_scale = scale * PF_LOG2E * (fp8 ? k_scale : 1.f);
-    // f16 queries are pre-scaled in f16 (see prefill_impl)
-    return q_dtype == KIND_BF16 || std::fabs(s_scale) <= 1.f;
+    return specialised_shape(hq, hkv, d, bs) && q_prescale_ok(q_dtype, kv_dtype, scale, k_scale);
 }
 
 int32_t launch_prefix_partials(const void* q, const void* kc, const void* vc, const int32_t* bt,

@@ -754,6 +754,54 @@ __device__ __forceinline__ void prefill_body(PrefillArgs a, const int32_t* __res
         }
 }
 
+// ---- launch arguments (host) ----
+
+// Workgroups of the chunked-prefill mode before the KV split: an upper bound
+// of the query tiles (sum_s ceil(n_s / QT) <= T / QT + num_seqs, QT = PP_ROWS
+// / G query tokens a tile) times the kv heads.  Workgroups past a
+// sequence's tiles find none and leave at once.
+inline int64_t chunk_base_wgs(int64_t num_tokens, int64_t num_seqs, int64_t hq, int64_t hkv) {
+    const int64_t QT = PP_ROWS / (hq / hkv);
+    return ((num_tokens + QT - 1) / QT + num_seqs) * hkv;
+}
+
+// Arguments of the chunked-prefill mode without a KV split: num_seqs
+// sequences whose new tokens are q rows query_start_loc[s] ..
+// query_start_loc[s + 1] - 1.  The grid is base_wgs workgroups.
+inline PrefillArgs chunk_mode_args(void* out, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                                   const int32_t* seq_lens, const int32_t* qsl, int64_t num_seqs, int64_t hq,
+                                   int64_t hkv, int64_t maxb, float scale, int32_t kv_dtype, float k_scale,
+                                   float v_scale, int64_t base_wgs) {
+    PrefillArgs a{};
+    a.out = out;
+    a.q = static_cast<const uint16_t*>(q);
+    a.k_cache = kc;
+    a.v_cache = vc;
+    a.block_tables = bt;
+    a.seq_lens = seq_lens;
+    a.query_start_loc = qsl;
+    a.num_seqs = static_cast<int32_t>(num_seqs);
+    a.num_q_heads = static_cast<int32_t>(hq);
+    a.num_kv_heads = static_cast<int32_t>(hkv);
+    a.max_blocks = static_cast<int32_t>(maxb);
+    const bool fp8 = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
+    a.s_scale = scale * PF_LOG2E * (fp8 ? k_scale : 1.f);
+    a.v_scale = fp8 ? v_scale : 1.f;
+    a.splits = 1;
+    a.base_wgs = static_cast<int32_t>(base_wgs);
+    a.part_stride = 1;
+    a.part_base = 0;
+    return a;
+}
+
+// Whether the MFMA kernel takes f16 queries at this scale: it multiplies the
+// queries by s_scale in the q type, and f16 could overflow past 1 (bf16 has
+// the float range)
+inline bool q_prescale_ok(int32_t q_dtype, int32_t kv_dtype, float scale, float k_scale) {
+    const bool fp8 = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
+    return q_dtype == KIND_BF16 || std::fabs(scale * PF_LOG2E * (fp8 ? k_scale : 1.f)) <= 1.f;
+}
+
 // ---- the shared-prefix mode's launch (host) ----
 
 // Workgroups of the shared-prefix mode before the KV split: the query tiles

@@ -324,29 +324,20 @@ inline Result<void> paged_attention_step(const DeviceStepMetadata& m, void* out,
     const float scale = p.scale;
     const bool fp8 = kv == DType::FP8E4M3 || kv == DType::FP8E5M2;
     const float ks = fp8 ? k_scale : 1.0f, vs = fp8 ? v_scale : 1.0f;
-    // 2. prefill group, on the same stream as the decode group that follows.
-    // The decode grid holds one 512-register wave per SIMD, so a prefill
-    // workgroup (eight waves) cannot run beside it: on a second stream the
-    // prefill only fills in as decode waves retire, which measured slower
-    // than running the two groups in series.
-    if (m.num_prefill_seqs > 0) {
-        const Result<void> r = check(rllm_paged_attention_prefill_ex(
-            out, q, key_cache, value_cache, m.prefill_block_tables, m.prefill_seq_lens, m.prefill_query_start_loc,
-            m.num_prefill_seqs, m.num_prefill_tokens, hq, hkv, d, bs, m.prefill_max_blocks, scale, a, c, ks, vs, st));
-        if (r.is_err()) return r;
-    }
-    // 3. decode group: its tokens follow the prefill tokens
-    if (m.num_decode_seqs > 0) {
-        const size_t esz = 2;
-        const size_t row = static_cast<size_t>(hq * d) * esz;
-        const size_t off = static_cast<size_t>(m.num_prefill_tokens) * row;
-        const Result<void> r = check(rllm_paged_attention_decode_ex(
-            static_cast<uint8_t*>(out) + off, static_cast<const uint8_t*>(q) + off, key_cache, value_cache,
-            m.decode_block_tables, m.decode_seq_lens, m.num_decode_seqs, hq, hkv, d, bs, m.decode_max_blocks, scale,
-            a, c, ks, vs, 0, nullptr, 0, st));
-        if (r.is_err()) return r;
-    }
-    return Result<void>::ok();
+    // 2. attention: the prefill group (its tokens first) and the decode
+    // group (one token each, after them) in one call.  With 16-bit caches and
+    // a prefill group of at most half as many workgroups as CUs, the library
+    // runs both in one launch, the prefill workgroups on their own CUs beside
+    // the stream decode; otherwise it runs them in series.  (A decode wave per
+    // SIMD leaves no room for an 8-wave prefill workgroup on the same CU, so a
+    // prefill on a second stream only fills in as decode waves retire.)
+    const size_t row = static_cast<size_t>(hq * d) * 2;
+    const size_t off = static_cast<size_t>(m.num_prefill_tokens) * row;
+    return check(rllm_paged_attention_mixed_ex(
+        out, q, m.prefill_block_tables, m.prefill_seq_lens, m.prefill_query_start_loc, m.num_prefill_seqs,
+        m.num_prefill_tokens, m.prefill_max_blocks, static_cast<uint8_t*>(out) + off,
+        static_cast<const uint8_t*>(q) + off, m.decode_block_tables, m.decode_seq_lens, m.num_decode_seqs,
+        m.decode_max_blocks, key_cache, value_cache, hq, hkv, d, bs, scale, a, c, ks, vs, st));
 }
 
 }  // namespace kernels

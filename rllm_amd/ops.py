@@ -166,6 +166,50 @@ def paged_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     return out
 
 
+def paged_mixed(prefill_q: torch.Tensor, prefill_block_tables: torch.Tensor, prefill_seq_lens: torch.Tensor,
+                query_start_loc: torch.Tensor, decode_q: torch.Tensor, decode_block_tables: torch.Tensor,
+                decode_seq_lens: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, scale: float, *,
+                kv_dtype: Optional[int] = None, k_scale: float = 1.0, v_scale: float = 1.0,
+                prefill_out: Optional[torch.Tensor] = None, decode_out: Optional[torch.Tensor] = None,
+                validate: bool = True, stream: Optional[torch.cuda.Stream] = None):
+    """One step's attention over a mixed batch through rllm_paged_attention_mixed_ex:
+    the prefill group (as paged_prefill's arguments) and the decode group (as
+    paged_decode's) over the same caches.  Returns (prefill_out, decode_out)."""
+    T, hq, d = prefill_q.shape
+    Bp = prefill_seq_lens.shape[0]
+    Bd = decode_q.shape[0]
+    _check_common(prefill_q, k_cache, v_cache, prefill_block_tables, prefill_seq_lens, Bp)
+    _check_common(decode_q, k_cache, v_cache, decode_block_tables, decode_seq_lens, Bd)
+    if decode_q.shape[1:] != (hq, d) or decode_q.dtype != prefill_q.dtype:
+        raise ValueError("the two groups' queries must have the same heads, head_dim and dtype")
+    if query_start_loc.dtype != torch.int32 or query_start_loc.shape != (Bp + 1,) or \
+            query_start_loc.device != prefill_q.device:
+        raise ValueError("query_start_loc must be int32 [num_prefill_seqs + 1] on the device of q")
+    nb, hkv, d2, bs = k_cache.shape
+    kv = _kv_code(k_cache, kv_dtype)
+    qd = _TORCH_16[prefill_q.dtype]
+    if kv in (DTYPE_F16, DTYPE_BF16) and kv != qd:
+        raise TypeError("a 16-bit cache must have the dtype of q")
+    if validate:
+        validate_tables(prefill_block_tables, prefill_seq_lens, nb, bs)
+        validate_tables(decode_block_tables, decode_seq_lens, nb, bs)
+        qsl = query_start_loc.detach().cpu()
+        if int(qsl[0]) != 0 or int(qsl[-1]) != T or bool((qsl[1:] < qsl[:-1]).any()):
+            raise ValueError("query_start_loc must rise from 0 to num_prefill_tokens")
+    if prefill_out is None:
+        prefill_out = torch.empty_like(prefill_q)
+    if decode_out is None:
+        decode_out = torch.empty_like(decode_q)
+    for o, ref in ((prefill_out, prefill_q), (decode_out, decode_q)):
+        if o.shape != ref.shape or o.dtype != ref.dtype or not o.is_contiguous() or o.device != ref.device:
+            raise ValueError("outputs must be contiguous tensors like their queries")
+    call("rllm_paged_attention_mixed_ex", _ptr(prefill_out), _ptr(prefill_q), _ptr(prefill_block_tables),
+         _ptr(prefill_seq_lens), _ptr(query_start_loc), Bp, T, prefill_block_tables.shape[1], _ptr(decode_out),
+         _ptr(decode_q), _ptr(decode_block_tables), _ptr(decode_seq_lens), Bd, decode_block_tables.shape[1],
+         _ptr(k_cache), _ptr(v_cache), hq, hkv, d, bs, scale, qd, kv, k_scale, v_scale, _stream(stream))
+    return prefill_out, decode_out
+
+
 def reshape_and_cache(new_key: torch.Tensor, new_value: torch.Tensor, k_cache: torch.Tensor,
                       v_cache: torch.Tensor, slot_mapping: torch.Tensor, *,
                       kv_dtype: Optional[int] = None, k_scale: float = 1.0, v_scale: float = 1.0,
