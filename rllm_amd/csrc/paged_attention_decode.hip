@@ -832,17 +832,43 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(DecodeArgs a) {
     const int64_t row = static_cast<int64_t>(s) * a.num_q_heads + hq;
     const float* ml = a.part_ml + row * a.max_parts * 2;
     const float* po = a.part_out + row * a.max_parts * D;
+    // partitions are read RB at a time, every load of a batch issued before
+    // any is used (the cascade's rows have at most 16); the sum runs in
+    // partition order whatever the batching
+    constexpr int RB = 8;
+    float m[RB], l[RB], v[RB][PER_LANE];
+    auto load = [&](int p0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            // past the row's partitions: read its last one again (always in
+            // bounds), weight it as nothing
+            const int pi = min(p0 + i, parts - 1);
+            const bool in = p0 + i < parts;
+            const float mm = ml[2 * pi], ll = ml[2 * pi + 1];
+            m[i] = in ? mm : -INFINITY;
+            l[i] = in ? ll : 0.f;
+#pragma unroll
+            for (int k = 0; k < PER_LANE; ++k) v[i][k] = po[pi * D + threadIdx.x + 64 * k];
+        }
+    };
+    load(0);
     float M = -INFINITY;
-    for (int p = 0; p < parts; ++p) M = fmaxf(M, ml[2 * p]);
+#pragma unroll
+    for (int i = 0; i < RB; ++i) M = fmaxf(M, m[i]);
+    for (int p = RB; p < parts; ++p) M = fmaxf(M, ml[2 * p]);
     float L = 0.f, acc[PER_LANE];
 #pragma unroll
     for (int k = 0; k < PER_LANE; ++k) acc[k] = 0.f;
-    for (int p = 0; p < parts; ++p) {
-        const float mp = ml[2 * p];
-        const float f = (mp == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mp - M) * ml[2 * p + 1];
-        L += f;
+    for (int p0 = 0; p0 < parts; p0 += RB) {
+        if (p0 > 0) load(p0);
 #pragma unroll
-        for (int k = 0; k < PER_LANE; ++k) acc[k] = fmaf(f, po[p * D + threadIdx.x + 64 * k], acc[k]);
+        for (int i = 0; i < RB; ++i) {
+            if (p0 + i >= parts) break;
+            const float f = (m[i] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[i] - M) * l[i];
+            L += f;
+#pragma unroll
+            for (int k = 0; k < PER_LANE; ++k) acc[k] = fmaf(f, v[i][k], acc[k]);
+        }
     }
 #pragma unroll
     for (int k = 0; k < PER_LANE; ++k) {
@@ -1455,7 +1481,7 @@ struct Kernels {
     const void* stream4_small;   // same with SMALL_SHARE_PF_V V blocks in flight (null if none)
     const void* reduce;
     const void* cascade;   // cascade_kernel (16-bit caches; null for FP8)
-    const void* mixed;     // mixed_kernel (16-bit caches; null for FP8)
+    const void* mixed;     // mixed_kernel
 };
 
 // V blocks in flight of the small-share stream kernel: a launch of at least
@@ -1476,11 +1502,8 @@ Kernels kernels_of() {
     if constexpr (KVKIND == QKIND && G <= 4)
         small = reinterpret_cast<const void*>(
             &decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB_WIDE, SMALL_SHARE_PF_V>);
-    const void* mixed = nullptr;
-    if constexpr (KVKIND == QKIND) {
-        cascade = reinterpret_cast<const void*>(&cascade_kernel<QKIND, KVKIND, D, G>);
-        mixed = reinterpret_cast<const void*>(&mixed_kernel<QKIND, KVKIND, D, G>);
-    }
+    if constexpr (KVKIND == QKIND) cascade = reinterpret_cast<const void*>(&cascade_kernel<QKIND, KVKIND, D, G>);
+    const void* mixed = reinterpret_cast<const void*>(&mixed_kernel<QKIND, KVKIND, D, G>);
     return {reinterpret_cast<const void*>(&decode_kernel<QKIND, KVKIND, D, G>),
             reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, 1>),
             reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB_WIDE>),
@@ -1757,15 +1780,18 @@ int32_t decode_prefix_impl(void* out, const void* q, const void* kc, const void*
 
 // Mixed batch of one step: the prefill group (chunks of new tokens on their
 // cached context) and the decode group (one token each) over the same cache.
-// 16-bit caches with few enough prefill workgroups run both in one
-// mixed_kernel launch: the unsplit prefill workgroups on their own CUs, the
-// stream decode on the others (MIXED_DECODE_WAVES a workgroup, two per
-// SIMD).  Otherwise the prefill and the decode run in series, as their own
-// entry points do.
+// With few enough prefill workgroups both run in one mixed_kernel launch: the
+// unsplit prefill workgroups on their own CUs, the stream decode on the
+// others, MIXED_DECODE_WAVES a workgroup for 16-bit caches (one per SIMD:
+// 112.6 us at the step's shape against 118.8 us with two per SIMD) and
+// MIXED_DECODE_WAVES_FP8 for FP8 caches (two per SIMD, as their stream decode
+// runs: a wave converts every byte it reads).  Otherwise the prefill and the
+// decode run in series, as their own entry points do.
 #ifndef RLLM_MIXED_DECODE_WAVES
 #define RLLM_MIXED_DECODE_WAVES 4
 #endif
 constexpr int64_t MIXED_DECODE_WAVES = RLLM_MIXED_DECODE_WAVES;
+constexpr int64_t MIXED_DECODE_WAVES_FP8 = 8;
 // The prefill group may take at most this share of the CUs (the decode needs
 // the rest to stream at full rate); a larger group runs in series.
 constexpr int64_t MIXED_MAX_PREFILL_CU_DIV = 2;
@@ -1805,11 +1831,12 @@ int32_t mixed_impl(void* p_out, const void* p_q, const int32_t* p_bt, const int3
 
     // the stream decode over the CUs the prefill workgroups leave free
     const int64_t free_cus = cus - pw;
+    const bool fp8 = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
+    const int64_t dpw = fp8 ? MIXED_DECODE_WAVES_FP8 : MIXED_DECODE_WAVES;
     const int max_waves = max_resident_waves();
     if (max_waves <= 0) return (int32_t)hipErrorInvalidDevice;
     const int64_t nw = std::min<int64_t>(
-        max_waves, stream_waves(d_num_seqs, hkv, d_maxb, MIXED_DECODE_WAVES * free_cus, 4 * free_cus,
-                                MIXED_DECODE_WAVES <= 4));
+        max_waves, stream_waves(d_num_seqs, hkv, d_maxb, dpw * free_cus, 4 * free_cus, dpw <= 4));
     const int64_t ws_bytes = nw > 1 ? stream_ws_bytes(max_waves, nw, G, d) : 0;
     void* ws = nullptr;
     if (ws_bytes > 0) {
@@ -1829,8 +1856,8 @@ int32_t mixed_impl(void* p_out, const void* p_q, const int32_t* p_bt, const int3
     da.num_q_heads = static_cast<int32_t>(hq);
     da.num_kv_heads = static_cast<int32_t>(hkv);
     da.max_blocks = static_cast<int32_t>(d_maxb);
-    da.s_scale = scale * LOG2E;   // 16-bit caches only
-    da.v_scale = 1.0f;
+    da.s_scale = scale * LOG2E * (fp8 ? k_scale : 1.0f);
+    da.v_scale = fp8 ? v_scale : 1.0f;
     da.num_waves = static_cast<int32_t>(nw);
     if (ws_bytes > 0) {
         da.arrivals = static_cast<uint32_t*>(ws);
@@ -1839,11 +1866,11 @@ int32_t mixed_impl(void* p_out, const void* p_q, const int32_t* p_bt, const int3
     }
     PrefillArgs pa = chunk_mode_args(p_out, p_q, kc, vc, p_bt, p_seq_lens, p_qsl, p_num_seqs, hq, hkv, p_maxb, scale,
                                      kv_dtype, k_scale, v_scale, pw);
-    const int64_t grid = pw + (nw + MIXED_DECODE_WAVES - 1) / MIXED_DECODE_WAVES;
+    const int64_t grid = pw + (nw + dpw - 1) / dpw;
     RLLM_CHECK_ARG(grid <= INT32_MAX);
     const int32_t* bt_arg = p_bt;
-    int32_t pw32 = static_cast<int32_t>(pw), dpw = static_cast<int32_t>(MIXED_DECODE_WAVES);
-    void* args[] = {&pa, const_cast<int32_t**>(&bt_arg), &da, &pw32, &dpw};
+    int32_t pw32 = static_cast<int32_t>(pw), dpw32 = static_cast<int32_t>(dpw);
+    void* args[] = {&pa, const_cast<int32_t**>(&bt_arg), &da, &pw32, &dpw32};
     RLLM_TRY(hipLaunchKernel(kern.mixed, dim3(static_cast<unsigned>(grid)), dim3(PP_THREADS), args, 0,
                              as_stream(stream)));
     return 0;
