@@ -164,8 +164,8 @@ int32_t rllm_paged_attention_decode_ex(void *output, const void *query, const vo
  *             finite values.  0 runs the plain decode.
  * The prefix's keys and values are read once per kv head for the whole
  * batch, with matrix cores; each sequence's blocks past the prefix are
- * attended separately (in the same kernel launch for 16-bit caches), and a
- * reduction merges the two in the log-sum-exp domain.  The result equals rllm_paged_attention_decode_ex's within
+ * attended separately (in the same kernel launch), and a reduction merges
+ * the two in the log-sum-exp domain.  The result equals rllm_paged_attention_decode_ex's within
  * rounding.  Shapes outside the tuned set (head_dim 64 / 128, block size 16,
  * GQA 1 / 2 / 4 / 8), and f16 queries whose scale * log2(e) (* k_scale)
  * exceeds 1, run the plain decode.  Scratch is library-owned per (device,

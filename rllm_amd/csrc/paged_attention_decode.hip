@@ -1480,7 +1480,7 @@ struct Kernels {
     const void* stream4;   // STREAM_WPB_WIDE waves per workgroup
     const void* stream4_small;   // same with SMALL_SHARE_PF_V V blocks in flight (null if none)
     const void* reduce;
-    const void* cascade;   // cascade_kernel (16-bit caches; null for FP8)
+    const void* cascade;   // cascade_kernel
     const void* mixed;     // mixed_kernel
 };
 
@@ -1502,7 +1502,7 @@ Kernels kernels_of() {
     if constexpr (KVKIND == QKIND && G <= 4)
         small = reinterpret_cast<const void*>(
             &decode_stream_kernel<QKIND, KVKIND, D, G, STREAM_WPB_WIDE, SMALL_SHARE_PF_V>);
-    if constexpr (KVKIND == QKIND) cascade = reinterpret_cast<const void*>(&cascade_kernel<QKIND, KVKIND, D, G>);
+    cascade = reinterpret_cast<const void*>(&cascade_kernel<QKIND, KVKIND, D, G>);
     const void* mixed = reinterpret_cast<const void*>(&mixed_kernel<QKIND, KVKIND, D, G>);
     return {reinterpret_cast<const void*>(&decode_kernel<QKIND, KVKIND, D, G>),
             reinterpret_cast<const void*>(&decode_stream_kernel<QKIND, KVKIND, D, G, 1>),
@@ -1678,9 +1678,8 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
 // partial in the first slots; the partitioned decode attends every
 // sequence's blocks past the prefix into the next slots; the reduction
 // merges them.  The prefix's K and V are then read once per kv head instead
-// of once per sequence.  With 16-bit caches both run in one cascade_kernel
-// launch; FP8 caches launch them in series.  Shapes or scalings the MFMA
-// kernel does not take run the plain decode.
+// of once per sequence.  Both run in one cascade_kernel launch.  Shapes or
+// scalings the MFMA kernel does not take run the plain decode.
 constexpr int64_t CASCADE_MAX_SUFFIX_PARTS = 8;   // suffix partitions per row, at most
 
 // Waves per suffix workgroup of cascade_kernel: the suffix items spread over
@@ -1753,28 +1752,21 @@ int32_t decode_prefix_impl(void* out, const void* q, const void* kc, const void*
     a.block_offset = static_cast<int32_t>(prefix_blocks);
     a.part_offset = static_cast<int32_t>(S);
     const int64_t items = num_seqs * hkv * suffix_parts;
-    if (kern.cascade) {
-        // one launch: the prefix workgroups first, then the suffix waves
-        const int64_t pw = prefix_base_wgs(num_seqs, hq, hkv) * S;
-        int32_t dpw = cascade_waves_per_wg(items, pw);
-        const int64_t grid = pw + (items + dpw - 1) / dpw;
-        RLLM_CHECK_ARG(grid <= INT32_MAX);
-        PrefillArgs pa = prefix_mode_args(q, kc, vc, bt, seq_lens, num_seqs, hq, hkv, prefix_blocks, scale,
-                                          kv_dtype, k_scale, v_scale, S, part_out, part_ml, max_parts);
-        const int32_t* bt_arg = bt;
-        int32_t pw32 = static_cast<int32_t>(pw), items32 = static_cast<int32_t>(items);
-        void* args[] = {&pa, const_cast<int32_t**>(&bt_arg), &a, &pw32, &items32, &dpw};
-        RLLM_TRY(hipLaunchKernel(kern.cascade, dim3(static_cast<unsigned>(grid)), dim3(PP_THREADS), args, 0, st));
-    } else {
-        // FP8 caches, in series on `stream`: running the prefix partials on a
-        // second stream beside the suffix decode measured slower (config 4a
-        // 51.7 -> 59.9 us; the fork and join events cost 6 and 12 us)
-        rc = launch_prefix_partials(q, kc, vc, bt, seq_lens, num_seqs, hq, hkv, d, prefix_blocks, scale, q_dtype,
-                                    kv_dtype, k_scale, v_scale, S, part_out, part_ml, max_parts, st);
-        if (rc) return rc;
-        rc = launch(kern.part, dim3(static_cast<unsigned>(items)), a, st);
-        if (rc) return rc;
-    }
+    // one launch: the prefix workgroups first, then the suffix waves.  (The
+    // two as separate kernels on two streams measured slower than in series,
+    // config 4a 59.9 against 51.7 us: the fork and join events cost 6 and 12
+    // us; in one launch 38-40 us.)
+    RLLM_CHECK_ARG(kern.cascade);
+    const int64_t pw = prefix_base_wgs(num_seqs, hq, hkv) * S;
+    int32_t dpw = cascade_waves_per_wg(items, pw);
+    const int64_t grid = pw + (items + dpw - 1) / dpw;
+    RLLM_CHECK_ARG(grid <= INT32_MAX);
+    PrefillArgs pa = prefix_mode_args(q, kc, vc, bt, seq_lens, num_seqs, hq, hkv, prefix_blocks, scale, kv_dtype,
+                                      k_scale, v_scale, S, part_out, part_ml, max_parts);
+    const int32_t* bt_arg = bt;
+    int32_t pw32 = static_cast<int32_t>(pw), items32 = static_cast<int32_t>(items);
+    void* args[] = {&pa, const_cast<int32_t**>(&bt_arg), &a, &pw32, &items32, &dpw};
+    RLLM_TRY(hipLaunchKernel(kern.cascade, dim3(static_cast<unsigned>(grid)), dim3(PP_THREADS), args, 0, st));
     return launch(kern.reduce, dim3(static_cast<unsigned>(rows)), a, st);
 }
 
