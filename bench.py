@@ -18,12 +18,15 @@ roofline   = algorithmic bytes / average decode-call duration measured with HIP
 cpu_baseline = the CPU oracle's fp32 decode (C, std threads) on the same
              inputs, timed on this host's cores (oracle/, checker only)
 
-The default run (config 2, no --op / --tp / --partition) adds two more lines
+The default run (config 2, no --op / --tp / --partition) adds four more lines
 to the same JSON object, each timed the same way with the same --steps /
 --warmup: "prefill_config5" (the MFMA chunked prefill of config 5, roofline
 against the dense bf16 MFMA peak, with its own CPU baseline) and
 "fp8_decode_config3" (decode over config 3's FP8-E4M3 cache, values drawn on
-the GPU, roofline against HBM peak).  --no-extra leaves them out.
+the GPU, roofline against HBM peak), "cascade_decode_config4a" (config 4a
+through the cascade decode over its 64 shared blocks, roofline on distinct
+bytes) and "mixed_step" (the C++ step layer's mixed prefill + decode layer
+step, us per step, lower is better).  --no-extra leaves them out.
 
 --calibrate-copy-mib N runs the library's block copy over N MiB three times
 after the timed region, so a counter run can scale FETCH_SIZE/WRITE_SIZE.
@@ -241,6 +244,29 @@ def bench_prefill(args, w, lib, dev, kv="bf16", steps=None, warmup=None, calibra
         res["cpu_baseline"] = cpu_baseline_prefill(w, qb, kb, vb)
     del pools, q, out
     return res
+
+
+def step_bench_path() -> str:
+    return os.path.join(os.path.dirname(os.path.abspath(__file__)), "rllm_amd", "host", "_build", "step_bench")
+
+
+def run_step_bench(args):
+    """The mixed serving step (rllm_amd/host/step_bench: metadata upload,
+    fused RoPE + cache write, one attention launch over config 2's decode
+    batch plus a 512-token chunk) as a child process with the same --steps /
+    --warmup; its JSON line, or None when the program is not built or fails."""
+    import subprocess
+    exe = step_bench_path()
+    if not os.path.exists(exe):
+        return None
+    r = subprocess.run([exe, "--steps", str(args.steps), "--warmup", str(args.warmup)], capture_output=True,
+                       text=True, timeout=300)
+    if r.returncode != 0:
+        return None
+    for line in r.stdout.splitlines():
+        if line.startswith("{"):
+            return json.loads(line)
+    return None
 
 
 def cpu_baseline_prefill(w, qb, kb, vb):
@@ -911,7 +937,7 @@ def main() -> int:
     if args.op == "step":
         # the C++ program runs as a child process (nothing here has touched the GPU)
         import subprocess
-        exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "rllm_amd", "host", "_build", "step_bench")
+        exe = step_bench_path()
         if not os.path.exists(exe):
             print(f"{exe} is not built; run __graft_entry__.build()", file=sys.stderr)
             return 2
@@ -965,6 +991,12 @@ def main() -> int:
         torch.cuda.empty_cache()
         res["fp8_decode_config3"] = bench_decode(args, workloads.config(3), lib, dev, cpu=False,
                                                  device_values=True, calibrate=False)
+        # config 4a through the cascade decode over its shared prefix, and the
+        # mixed serving step (C++ step layer, a child process)
+        torch.cuda.empty_cache()
+        res["cascade_decode_config4a"] = bench_decode(argparse.Namespace(**{**vars(args), "cascade": True}),
+                                                      workloads.config(4), lib, dev, cpu=False, calibrate=False)
+        res["mixed_step"] = run_step_bench(args)
     print(json.dumps(res), flush=True)
     return 0
 
