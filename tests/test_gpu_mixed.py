@@ -211,3 +211,59 @@ def test_mixed_repeated_calls_give_the_same_bits(dev):
     runs = [run_mixed(dev, e, O.BF16, O.BF16, 0.088, label=f"repeat {i}") for i in range(3)]
     for po, do in runs[1:]:
         assert np.array_equal(po, runs[0][0]) and np.array_equal(do, runs[0][1])
+
+
+def test_mixed_graph_replays_match_eager(dev):
+    """A serving loop captures its step in a hipGraph.  After one eager call
+    on the capture stream (which gives that stream its decode scratch), the
+    captured call is the one-launch kernel, and every replay (with other work
+    queued between them) gives the eager call's bits.  Captured on a stream
+    without scratch, the call runs the two groups in series with the
+    capture-safe paths and still matches the oracle."""
+    rng = np.random.default_rng(1904)
+    c = mixed_case(rng, [300], [700], rng.integers(128, 1500, size=24), 32, 8, 128)
+    e = encode(c, O.BF16, O.BF16)
+    scale = 1 / np.sqrt(128)
+    rp, rd = oracle_ref(e, O.BF16, O.BF16, scale)
+    g = to_dev(e, dev, O.BF16, O.BF16)
+    po, do = torch.zeros_like(g["qp"]), torch.zeros_like(g["qd"])
+
+    def call(po_, do_):
+        ops.paged_mixed(g["qp"], g["p_bt"], g["p_sl"], g["qsl"], g["qd"], g["d_bt"], g["d_sl"], g["k"], g["v"], scale,
+                        prefill_out=po_, decode_out=do_, validate=False)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    log_case("graph mixed eager on the capture stream")
+    with torch.cuda.stream(side):
+        call(po, do)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    eager_p, eager_d = po.clone(), do.clone()
+    assert_close(f32(eager_p), rp, TOL_BF16, "mixed eager prefill")
+    assert_close(f32(eager_d), rd, TOL_BF16, "mixed eager decode")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        call(po, do)
+    torch.cuda.synchronize()
+    other = torch.zeros_like(g["qd"])
+    for r in range(3):
+        po.zero_()
+        do.zero_()
+        log_case(f"graph mixed replay {r}")
+        graph.replay()
+        # eager work between the replays
+        ops.paged_decode(g["qd"], g["k"], g["v"], g["d_bt"], g["d_sl"], scale, out=other, validate=False)
+        torch.cuda.synchronize()
+        assert torch.equal(po, eager_p) and torch.equal(do, eager_d), f"replay {r} differs from the eager call"
+    # a stream that has no decode scratch: the capture runs the series path
+    g2 = torch.cuda.CUDAGraph()
+    po2, do2 = torch.zeros_like(po), torch.zeros_like(do)
+    log_case("graph mixed capture without scratch")
+    with torch.cuda.graph(g2, stream=torch.cuda.Stream()):
+        call(po2, do2)
+    for r in range(2):
+        g2.replay()
+        torch.cuda.synchronize()
+        assert_close(f32(po2), rp, TOL_BF16, f"mixed captured without scratch, prefill, replay {r}")
+        assert_close(f32(do2), rd, TOL_BF16, f"mixed captured without scratch, decode, replay {r}")
