@@ -757,12 +757,16 @@ __device__ __forceinline__ void prefill_body(PrefillArgs a, const int32_t* __res
 // ---- launch arguments (host) ----
 
 // Workgroups of the chunked-prefill mode before the KV split: an upper bound
-// of the query tiles (sum_s ceil(n_s / QT) <= T / QT + num_seqs, QT = PP_ROWS
-// / G query tokens a tile) times the kv heads.  Workgroups past a
-// sequence's tiles find none and leave at once.
+// of the query tiles times the kv heads (QT = PP_ROWS / G query tokens a
+// tile).  ceil(n / QT) <= (n - 1) / QT + 1 for every n >= 0, so the tiles of
+// num_seqs sequences with num_tokens in all number at most
+// (num_tokens - num_seqs) / QT + num_seqs (exact for one sequence); the
+// division truncates toward zero, which only loosens the bound when
+// num_tokens < num_seqs.  Workgroups past the tiles find none and leave at
+// once.
 inline int64_t chunk_base_wgs(int64_t num_tokens, int64_t num_seqs, int64_t hq, int64_t hkv) {
     const int64_t QT = PP_ROWS / (hq / hkv);
-    return ((num_tokens + QT - 1) / QT + num_seqs) * hkv;
+    return ((num_tokens - num_seqs) / QT + num_seqs) * hkv;
 }
 
 // Arguments of the chunked-prefill mode without a KV split: num_seqs
