@@ -325,10 +325,10 @@ inline Result<void> paged_attention_step(const DeviceStepMetadata& m, void* out,
     const bool fp8 = kv == DType::FP8E4M3 || kv == DType::FP8E5M2;
     const float ks = fp8 ? k_scale : 1.0f, vs = fp8 ? v_scale : 1.0f;
     // 2. attention: the prefill group (its tokens first) and the decode
-    // group (one token each, after them) in one call.  With 16-bit caches and
-    // a prefill group of at most half as many workgroups as CUs, the library
-    // runs both in one launch, the prefill workgroups on their own CUs beside
-    // the stream decode; otherwise it runs them in series.  (A decode wave per
+    // group (one token each, after them) in one call.  With a prefill group
+    // of at most half as many workgroups as CUs, the library runs both in one
+    // launch, the prefill workgroups on their own CUs beside the stream
+    // decode; otherwise it runs them in series.  (A decode wave per
     // SIMD leaves no room for an 8-wave prefill workgroup on the same CU, so a
     // prefill on a second stream only fills in as decode waves retire.)
     const size_t row = static_cast<size_t>(hq * d) * 2;
