@@ -211,3 +211,35 @@ def test_prefix_invalid_arguments(dev):
     bad[1, 0] = bt[0, 1]
     with pytest.raises(ValueError):
         ops.paged_decode_prefix(qt, kc, vc, ti(bad, torch.int32, dev), slt, 0.125, 2)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_prefix_random_sweep_vs_oracle(dev, seed):
+    """Random cascades: head_dim, GQA, kv heads, cache type, batch size,
+    prefix length and suffix lengths drawn per case, against the oracle's
+    plain decode of the aliased tables."""
+    rng = np.random.default_rng(3000 + seed)
+    D = int(rng.choice([64, 128]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    kind = int(rng.choice([O.BF16, O.F16]))
+    kv = kind if rng.random() < 0.7 else int(rng.choice([O.FP8_E4M3, O.FP8_E5M2]))
+    if kind == O.F16 and kv != kind:
+        kind = O.BF16
+    B = int(rng.integers(1, 120))
+    P = int(rng.integers(1, 80))
+    lo = int(rng.integers(0, 200))
+    q, k, v, bt, sl = prefix_case(rng, B, hkv * G, hkv, D, P, (lo, lo + int(rng.integers(1, 800))))
+    ks = vs = 1.0
+    if kv in (O.FP8_E4M3, O.FP8_E5M2):
+        top = 448.0 if kv == O.FP8_E4M3 else 57344.0
+        ks, vs = float(np.abs(k).max() / top), float(np.abs(v).max() / top)
+        kb = O.encode((k / np.float32(ks)).astype(np.float32), kv)
+        vb = O.encode((v / np.float32(vs)).astype(np.float32), kv)
+    else:
+        kb, vb = O.encode(k, kv), O.encode(v, kv)
+    qb = O.encode(q, kind)
+    scale = 1 / np.sqrt(D)
+    ref = oracle_ref(qb, kind, kb, vb, kv, bt, sl, scale, ks, vs)
+    got = run_prefix(dev, qb, kind, kb, vb, kv, bt, sl, scale, P, ks, vs, label=f"sweep {seed}")
+    assert_close(got, ref, TOL_BF16 if kv == kind else TOL_FP8, f"prefix sweep {seed}")

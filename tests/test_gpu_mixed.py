@@ -267,3 +267,34 @@ def test_mixed_graph_replays_match_eager(dev):
         torch.cuda.synchronize()
         assert_close(f32(po2), rp, TOL_BF16, f"mixed captured without scratch, prefill, replay {r}")
         assert_close(f32(do2), rd, TOL_BF16, f"mixed captured without scratch, decode, replay {r}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_mixed_random_sweep_vs_oracle(dev, seed):
+    """Random steps: head_dim, GQA, kv heads, cache type, the number and
+    lengths of the chunks and of the decode contexts drawn per case (some
+    large enough to run in series)."""
+    rng = np.random.default_rng(2000 + seed)
+    D = int(rng.choice([64, 128]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    kind = int(rng.choice([O.BF16, O.F16]))
+    kv = kind if rng.random() < 0.7 else int(rng.choice([O.FP8_E4M3, O.FP8_E5M2]))
+    if kind == O.F16 and kv != kind:
+        kind = O.BF16   # FP8 caches with bf16 queries (f16 queries are covered above)
+    bp = int(rng.integers(1, 5))
+    n_new = rng.integers(1, 700, size=bp)
+    cached = rng.integers(0, 1500, size=bp)
+    dec = rng.integers(0, 2500, size=int(rng.integers(1, 80)))
+    c = mixed_case(rng, n_new, cached, dec, hkv * G, hkv, D)
+    ks = vs = 1.0
+    if kv in (O.FP8_E4M3, O.FP8_E5M2):
+        top = 448.0 if kv == O.FP8_E4M3 else 57344.0
+        ks, vs = float(np.abs(c["k"]).max() / top), float(np.abs(c["v"]).max() / top)
+    e = encode(c, kind, kv, ks, vs)
+    scale = 1 / np.sqrt(D)
+    rp, rd = oracle_ref(e, kind, kv, scale, ks, vs)
+    po, do = run_mixed(dev, e, kind, kv, scale, ks, vs, label=f"sweep {seed}")
+    tol = TOL_BF16 if kv == kind else TOL_FP8
+    assert_close(po, rp, tol, f"mixed sweep {seed} prefill")
+    assert_close(do, rd, tol, f"mixed sweep {seed} decode")
