@@ -254,18 +254,25 @@ def run_step_bench(args):
     """The mixed serving step (rllm_amd/host/step_bench: metadata upload,
     fused RoPE + cache write, one attention launch over config 2's decode
     batch plus a 512-token chunk) as a child process with the same --steps /
-    --warmup; its JSON line, or None when the program is not built or fails."""
+    --warmup; its JSON line, or None when the program is not built, fails or
+    takes more than 300 s."""
     import subprocess
     exe = step_bench_path()
     if not os.path.exists(exe):
         return None
-    r = subprocess.run([exe, "--steps", str(args.steps), "--warmup", str(args.warmup)], capture_output=True,
-                       text=True, timeout=300)
+    try:
+        r = subprocess.run([exe, "--steps", str(args.steps), "--warmup", str(args.warmup)], capture_output=True,
+                           text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        return None
     if r.returncode != 0:
         return None
     for line in r.stdout.splitlines():
         if line.startswith("{"):
-            return json.loads(line)
+            try:
+                return json.loads(line)
+            except ValueError:
+                return None
     return None
 
 
