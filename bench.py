@@ -925,6 +925,8 @@ def main() -> int:
     ap.add_argument("--kv", default="bf16", choices=["bf16", "fp8_e4m3", "fp8_e5m2"],
                     help="config 5: KV cache dtype of the prefill line (FP8 written by the "
                          "library's cache write, scales amax / max finite); --op step: the step's cache dtype")
+    ap.add_argument("--chunk", type=int, default=512,
+                    help="--op step: new tokens of the step's prefill chunk (on 2048 cached tokens)")
     ap.add_argument("--prefill-seqs", type=int, default=0,
                     help="config 5: time only the first N sequences' chunks (1: one prompt, the small-batch "
                          "path that splits the KV range)")
@@ -949,7 +951,7 @@ def main() -> int:
             print(f"{exe} is not built; run __graft_entry__.build()", file=sys.stderr)
             return 2
         return subprocess.run([exe, "--steps", str(args.steps), "--warmup", str(args.warmup),
-                               "--kv", args.kv]).returncode
+                               "--kv", args.kv, "--prefill-new", str(args.chunk)]).returncode
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the decode path "
               "would shard by sequence / kv head with no exchange between GPUs", file=sys.stderr)

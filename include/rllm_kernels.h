@@ -189,7 +189,7 @@ int32_t rllm_paged_attention_decode_prefix_ex(void *output, const void *query, c
  * rllm_paged_attention_decode_ex's with partition_size 0 and no workspace
  * (decode_*), over the same caches, heads and scales.  The two groups'
  * outputs and queries are separate arrays (they may be two row ranges of one
- * buffer).  With the tuned shapes and a prefill group of at most half as
+ * buffer).  With the tuned shapes and a prefill group of at most 5/8 as
  * many workgroups as the GPU has CUs (256 query rows a workgroup: 64 tokens
  * at GQA 4), both groups run in one kernel launch, the prefill on its own CUs
  * beside the decode; otherwise, or when either group is empty, the two entry

@@ -1784,9 +1784,14 @@ int32_t decode_prefix_impl(void* out, const void* q, const void* kc, const void*
 #endif
 constexpr int64_t MIXED_DECODE_WAVES = RLLM_MIXED_DECODE_WAVES;
 constexpr int64_t MIXED_DECODE_WAVES_FP8 = 8;
-// The prefill group may take at most this share of the CUs (the decode needs
-// the rest to stream at full rate); a larger group runs in series.
-constexpr int64_t MIXED_MAX_PREFILL_CU_DIV = 2;
+// The prefill group may take at most MIXED_PREFILL_CU_NUM / MIXED_PREFILL_CU_DEN
+// of the CUs; a larger group runs in series (the decode on the CUs left would
+// take longer than the prefill's own launch).  Config 2's decode batch plus one
+// chunk on 2048 cached tokens, step times in one launch against in series:
+// 768 tokens (96 workgroups) 146 against 195 us, 1024 (128) 163 against 189,
+// 1280 (160) 190 against 221, 1536 (192) 246 against 219.
+constexpr int64_t MIXED_PREFILL_CU_NUM = 5;
+constexpr int64_t MIXED_PREFILL_CU_DEN = 8;
 
 int32_t mixed_impl(void* p_out, const void* p_q, const int32_t* p_bt, const int32_t* p_seq_lens,
                    const int32_t* p_qsl, int64_t p_num_seqs, int64_t p_num_tokens, int64_t p_maxb, void* d_out,
@@ -1819,7 +1824,7 @@ int32_t mixed_impl(void* p_out, const void* p_q, const int32_t* p_bt, const int3
     RLLM_CHECK_ARG(pick_kernels(q_dtype, kv_dtype, d, G, &kern));
     const int64_t cus = device_cus();
     const int64_t pw = chunk_base_wgs(p_num_tokens, p_num_seqs, hq, hkv);
-    if (!kern.mixed || cus <= 0 || pw > cus / MIXED_MAX_PREFILL_CU_DIV) return serial();
+    if (!kern.mixed || cus <= 0 || pw * MIXED_PREFILL_CU_DEN > cus * MIXED_PREFILL_CU_NUM) return serial();
 
     // the stream decode over the CUs the prefill workgroups leave free
     const int64_t free_cus = cus - pw;

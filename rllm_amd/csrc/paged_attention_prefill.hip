@@ -107,20 +107,57 @@ int32_t launch_prefill_d(int64_t D, int64_t G, const PrefillArgs& a, dim3 grid, 
     return (int32_t)hipErrorInvalidValue;
 }
 
-// KV splits for a launch of base_wgs workgroups over tables max_blocks wide:
-// enough to give every CU a workgroup, at most 8, and only while each split
-// keeps at least 4 of the widest row's 64-token tiles.
-int64_t prefill_splits(int64_t base_wgs, int64_t max_blocks) {
+// compute units of the current device (0 when unknown)
+int device_cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        return 1;
-    const int64_t want = static_cast<int64_t>(cus);
-    if (base_wgs >= want) return 1;
+        return 0;
+    return cus;
+}
+
+// KV splits for a launch of base_wgs workgroups over tables max_blocks wide:
+// enough to give every CU a workgroup, at most 8, and only while each split
+// keeps at least 4 of the widest row's 64-token tiles (the shared-prefix
+// partials of the cascade decode, which run beside its suffix work).
+int64_t prefill_splits(int64_t base_wgs, int64_t max_blocks) {
+    const int64_t want = device_cu_count();
+    if (want <= 0 || base_wgs >= want) return 1;
     int64_t sp = std::min<int64_t>(PF_MAX_SPLITS, (want + base_wgs - 1) / base_wgs);
     const int64_t tiles = (max_blocks + PF_NBT - 1) / PF_NBT;
     sp = std::min<int64_t>(sp, tiles / 4);
     return sp > 1 ? sp : 1;
+}
+
+// KV splits of the chunked prefill (prefill_impl): of the counts up to 8 that
+// keep at least 4 of the widest row's tiles a split, the one with the least
+// estimated time in tiles,
+//   rounds of the grid on the CUs x (the split's tiles + CHUNK_WG_COST)
+//   + CHUNK_MERGE_COST when split,
+// CHUNK_WG_COST standing for a workgroup's pipeline fill and epilogue and
+// CHUNK_MERGE_COST for the merge kernel (one config-5 prompt, 40 tiles split
+// 4 ways: 33 + 7 us).  A count is taken over a smaller one only when its
+// estimate is at least 10% lower.  Filling the CUs with one more round seldom
+// pays: one prompt of 768 new tokens (96 workgroups) split 3 ways makes 288
+// workgroups, two rounds on 256 CUs; split 2 ways, one.
+constexpr int64_t CHUNK_WG_COST = 3;
+constexpr int64_t CHUNK_MERGE_COST = 3;
+
+int64_t chunk_splits(int64_t base_wgs, int64_t max_blocks) {
+    const int64_t cus = device_cu_count();
+    if (cus <= 0 || base_wgs <= 0 || base_wgs >= cus) return 1;
+    const int64_t tiles = (max_blocks + PF_NBT - 1) / PF_NBT;
+    const int64_t max_sp = std::min<int64_t>(PF_MAX_SPLITS, tiles / 4);
+    int64_t best = 1, best_cost = tiles + CHUNK_WG_COST;
+    for (int64_t sp = 2; sp <= max_sp; ++sp) {
+        const int64_t rounds = (base_wgs * sp + cus - 1) / cus;
+        const int64_t cost = rounds * ((tiles + sp - 1) / sp + CHUNK_WG_COST) + CHUNK_MERGE_COST;
+        if (cost * 10 < best_cost * 9) {
+            best = sp;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 
 int32_t prefill_impl(void* out, const void* q, const void* kc, const void* vc, const int32_t* bt,
@@ -154,7 +191,7 @@ int32_t prefill_impl(void* out, const void* q, const void* kc, const void* vc, c
                                     k_scale, v_scale, nwg);
     // few workgroups (a small batch): split every row's KV range over up to
     // 8 workgroups and merge the partials in a second kernel
-    const int64_t splits = prefill_splits(nwg, maxb);
+    const int64_t splits = chunk_splits(nwg, maxb);
     a.splits = static_cast<int32_t>(splits);
     a.base_wgs = static_cast<int32_t>(nwg);
     const int64_t rows = num_tokens * hq;

@@ -157,7 +157,7 @@ def test_mixed_fp8_caches_vs_oracle(dev, fp8):
 
 @pytest.mark.parametrize("kv", [O.BF16, O.FP8_E4M3])
 def test_mixed_large_prefill_group_in_series_vs_oracle(dev, kv):
-    """Eight 512-token chunks take more than half the CUs (576 workgroups):
+    """Eight 512-token chunks take more than 5/8 of the CUs (576 workgroups):
     the groups run in series, the prefill split as its own entry point does."""
     rng = np.random.default_rng(1601 + kv)
     c = mixed_case(rng, [512] * 8, [256] * 8, rng.integers(1, 600, size=16), 32, 8, 64)
