@@ -167,8 +167,12 @@ int32_t rllm_paged_attention_decode_ex(void *output, const void *query, const vo
  * attended separately (in the same kernel launch), and a reduction merges
  * the two in the log-sum-exp domain.  The result equals rllm_paged_attention_decode_ex's within
  * rounding.  Shapes outside the tuned set (head_dim 64 / 128, block size 16,
- * GQA 1 / 2 / 4 / 8), and f16 queries whose scale * log2(e) (* k_scale)
- * exceeds 1, run the plain decode.  Scratch is library-owned per (device,
+ * GQA 1 / 2 / 4 / 8), f16 queries whose scale * log2(e) (* k_scale)
+ * exceeds 1, and batches whose prefix saves too little run the plain decode:
+ * the cascade is used when (num_seqs - 1) * num_prefix_blocks is at least
+ * 3/5 of num_seqs * (max_blocks_per_seq - num_prefix_blocks) and, times
+ * num_kv_heads, at least 10000 (the environment variable RLLM_CASCADE=always
+ * or =never overrides this, read on every call).  Scratch is library-owned per (device,
  * stream); calls on one stream must not be captured unless an eager call of
  * the same or a larger shape ran on that stream before (a capture with too
  * small a buffer runs the plain decode instead). */

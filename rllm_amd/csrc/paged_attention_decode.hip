@@ -45,6 +45,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -1679,8 +1681,35 @@ int32_t decode_impl(void* out, const void* q, const void* kc, const void* vc, co
 // sequence's blocks past the prefix into the next slots; the reduction
 // merges them.  The prefix's K and V are then read once per kv head instead
 // of once per sequence.  Both run in one cascade_kernel launch.  Shapes or
-// scalings the MFMA kernel does not take run the plain decode.
+// scalings the MFMA kernel does not take, and batches whose prefix saves too
+// little (cascade_pays), run the plain decode.
 constexpr int64_t CASCADE_MAX_SUFFIX_PARTS = 8;   // suffix partitions per row, at most
+
+// Whether the cascade beats the plain decode over the same tables.  It reads
+// the prefix once instead of once per sequence, (num_seqs - 1) * prefix_blocks
+// blocks fewer, but its prefix workgroups cost ~15 us however little they
+// attend and its suffix runs on the CUs they leave.  It is used when the
+// blocks saved are at least 3/5 of the suffix blocks (the table width past
+// the prefix, per sequence) and at least CASCADE_MIN_SAVED_TILES (block, kv
+// head) tiles.  Plain decode against the cascade, bf16, 32/8 heads, D 128,
+// tables of sequences x (shared + own) blocks, us per call:
+//   128 x (8 + 16)   30.2 against 31.9      128 x (12 + 16)  32.9 against 31.5
+//   16 x (64 + 16)   15.9 against 17.0      24 x (64 + 16)   23.0 against 17.3
+//   64 x (32 + 64)   50.2 against 51.1      64 x (64 + 64)   53.2 against 52.2
+//   64 x (8 + 128)   84.7 against 95.6      128 x (64 + 16)  66.1 against 32.7
+// RLLM_CASCADE=always or =never in the environment overrides the choice
+// (read on every call).
+constexpr int64_t CASCADE_MIN_SAVED_TILES = 10000;
+
+bool cascade_pays(int64_t num_seqs, int64_t hkv, int64_t maxb, int64_t prefix_blocks) {
+    if (const char* e = std::getenv("RLLM_CASCADE")) {
+        if (!std::strcmp(e, "always")) return true;
+        if (!std::strcmp(e, "never")) return false;
+    }
+    const int64_t saved = (num_seqs - 1) * prefix_blocks;
+    const int64_t suffix = num_seqs * (maxb - prefix_blocks);
+    return saved * 5 >= suffix * 3 && saved * hkv >= CASCADE_MIN_SAVED_TILES;
+}
 
 // Waves per suffix workgroup of cascade_kernel: the suffix items spread over
 // the CUs the prefix workgroups leave free, at most 8 a workgroup.  Config
@@ -1704,7 +1733,8 @@ int32_t decode_prefix_impl(void* out, const void* q, const void* kc, const void*
     RLLM_CHECK_ARG(q_dtype == KIND_F16 || q_dtype == KIND_BF16);
     RLLM_CHECK_ARG(kv_dtype == q_dtype || kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2);
     RLLM_CHECK_ARG(std::isfinite(scale) && std::isfinite(k_scale) && std::isfinite(v_scale));
-    if (prefix_blocks == 0 || !prefix_partials_supported(hq, hkv, d, bs, q_dtype, kv_dtype, scale, k_scale))
+    if (prefix_blocks == 0 || !prefix_partials_supported(hq, hkv, d, bs, q_dtype, kv_dtype, scale, k_scale) ||
+        !cascade_pays(num_seqs, hkv, maxb, prefix_blocks))
         return decode_impl(out, q, kc, vc, bt, seq_lens, num_seqs, hq, hkv, d, bs, maxb, scale, q_dtype, kv_dtype,
                            k_scale, v_scale, 0, nullptr, 0, stream);
     const int64_t G = hq / hkv;

@@ -9,7 +9,11 @@ sequence's own blocks separately and merges the two, so these tests compare
 it with the oracle's plain decode of the aliased tables (the oracle knows
 nothing of the prefix): shapes, cache types, contexts that end inside the
 prefix or right at its end, empty contexts, long suffixes split into several
-partitions, and config 4a at its own size."""
+partitions, and config 4a at its own size.
+
+The entry point runs the plain decode where the prefix saves too little; the
+tests of the cascade itself force it with RLLM_CASCADE=always, and
+test_prefix_auto_choice_follows_the_rule checks the choice."""
 import numpy as np
 import pytest
 import torch
@@ -22,6 +26,13 @@ from rllm_amd import ops, workloads
 
 pytestmark = pytest.mark.gpu
 TORCH = {O.BF16: torch.bfloat16, O.F16: torch.float16}
+
+
+@pytest.fixture(autouse=True)
+def _force_cascade(monkeypatch):
+    """These small batches would run the plain decode by the entry point's own
+    choice; the cascade kernel is what they test."""
+    monkeypatch.setenv("RLLM_CASCADE", "always")
 ABI = {O.F16: rllm_amd.DTYPE_F16, O.BF16: rllm_amd.DTYPE_BF16, O.FP8_E4M3: rllm_amd.DTYPE_FP8_E4M3,
        O.FP8_E5M2: rllm_amd.DTYPE_FP8_E5M2}
 
@@ -243,3 +254,33 @@ def test_prefix_random_sweep_vs_oracle(dev, seed):
     ref = oracle_ref(qb, kind, kb, vb, kv, bt, sl, scale, ks, vs)
     got = run_prefix(dev, qb, kind, kb, vb, kv, bt, sl, scale, P, ks, vs, label=f"sweep {seed}")
     assert_close(got, ref, TOL_BF16 if kv == kind else TOL_FP8, f"prefix sweep {seed}")
+
+
+@pytest.mark.parametrize("B,P,own,cascade", [
+    (9, 5, 4, False),      # saves 40 blocks: under the 10,000-tile floor
+    (128, 8, 16, False),   # saves 1,016 blocks, under 3/5 of the 2,048 suffix blocks
+    (32, 64, 16, True),    # saves 1,984 blocks (15,872 tiles), suffix 512
+    (64, 64, 16, True),
+], ids=["small", "short-prefix", "cascade-32", "cascade-64"])
+def test_prefix_auto_choice_follows_the_rule(dev, monkeypatch, B, P, own, cascade):
+    """Without RLLM_CASCADE the entry point runs the cascade only where the
+    prefix saves enough: the cascade when (B - 1) * P >= 3/5 * B * own and
+    (B - 1) * P * Hkv >= 10,000, else the plain decode.  Its output has the
+    forced cascade's bits or the plain decode's, as the rule says, and
+    RLLM_CASCADE=never gives the plain decode's."""
+    rng = np.random.default_rng(4100 + B + P)
+    q, k, v, bt, sl = prefix_case(rng, B, 32, 8, 128, P, (own * 16, own * 16))
+    assert bt.shape[1] == P + own
+    qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
+    scale = 1 / np.sqrt(128)
+    forced = run_prefix(dev, qb, O.BF16, kb, vb, O.BF16, bt, sl, scale, P, label=f"forced B={B}")
+    monkeypatch.delenv("RLLM_CASCADE")
+    auto = run_prefix(dev, qb, O.BF16, kb, vb, O.BF16, bt, sl, scale, P, label=f"auto B={B}")
+    monkeypatch.setenv("RLLM_CASCADE", "never")
+    never = run_prefix(dev, qb, O.BF16, kb, vb, O.BF16, bt, sl, scale, P, label=f"never B={B}")
+    plain = f32(ops.paged_decode(t16(qb, torch.bfloat16, dev), t16(kb, torch.bfloat16, dev),
+                                 t16(vb, torch.bfloat16, dev), ti(bt, torch.int32, dev), ti(sl, torch.int32, dev),
+                                 scale))
+    assert np.array_equal(never, plain)
+    assert np.array_equal(auto, forced if cascade else plain)
+    assert np.max(np.abs(forced - plain)) <= 2 ** -7 * max(1.0, float(np.abs(plain).max()))
