@@ -203,6 +203,13 @@ __global__ __launch_bounds__(ROPE_THREADS) void rope_cache_kernel(
     }
 
     const int32_t h = role;
+    // the group's slots, loaded before phase 1 so that their round trip
+    // overlaps its loads instead of following its LDS writes
+    int64_t sl = -1, s0 = -1;
+    if (threadIdx.x < ROPE_GROUP) {
+        s0 = slot_mapping[t0];
+        if (static_cast<int32_t>(threadIdx.x) < n_tok) sl = slot_mapping[t0 + threadIdx.x];
+    }
     const int32_t stride = head_dim + 8;   // LDS row in elements (16-byte pad)
     uint16_t* kl = lds;
     uint16_t* vl = lds + ROPE_GROUP * stride;
@@ -232,11 +239,9 @@ __global__ __launch_bounds__(ROPE_THREADS) void rope_cache_kernel(
     int32_t run = 1;
     if (threadIdx.x < ROPE_GROUP) {
         const int32_t tok = threadIdx.x;
-        const int64_t sl = tok < n_tok ? slot_mapping[t0 + tok] : -1;
         const int64_t blk = sl >= 0 ? sl / block_size : 0;
         const bool valid = sl >= 0 && blk < num_blocks;
         s_base[tok] = valid ? blk * row_elems * block_size + (sl - blk * block_size) : -1;
-        const int64_t s0 = slot_mapping[t0];
         run = n_tok == ROPE_GROUP && block_size % ROPE_GROUP == 0 && s0 >= 0 && s0 % ROPE_GROUP == 0 &&
               sl == s0 + tok && valid &&
               ((reinterpret_cast<uintptr_t>(key_cache) | reinterpret_cast<uintptr_t>(value_cache)) & 15) == 0;
