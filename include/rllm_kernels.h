@@ -193,13 +193,14 @@ int32_t rllm_paged_attention_decode_prefix_ex(void *output, const void *query, c
  * rllm_paged_attention_decode_ex's with partition_size 0 and no workspace
  * (decode_*), over the same caches, heads and scales.  The two groups'
  * outputs and queries are separate arrays (they may be two row ranges of one
- * buffer).  With the tuned shapes and a prefill group of at most 5/8 as
- * many workgroups as the GPU has CUs (256 query rows a workgroup: 64 tokens
- * at GQA 4), both groups run in one kernel launch, the prefill on its own CUs
- * beside the decode; otherwise, or when either group is empty, the two entry
- * points run in series.  Results equal the two entry
- * points' within rounding (the prefill group is never split over its KV
- * range here).  Scratch is the decode's library-owned stream workspace, per
+ * buffer).  With the tuned shapes both groups run in one kernel launch: the
+ * prefill workgroups (256 query rows each: 64 tokens at GQA 4) on their own
+ * CUs, the decode beside them on the other CUs, or, when the prefill takes
+ * more than half of the CUs, on every CU as the prefill leaves it.  Shapes
+ * outside the tuned set, f16 queries whose scale * log2(e) (* k_scale)
+ * exceeds 1, and an empty group run the two entry points in series.  Results
+ * equal the two entry points' within rounding (the prefill group is never
+ * split over its KV range in the one launch).  Scratch is the decode's library-owned stream workspace, per
  * (device, stream); a capture on a stream without it runs in series. */
 int32_t rllm_paged_attention_mixed_ex(void *prefill_output, const void *prefill_query,
                                       const int32_t *prefill_block_tables, const int32_t *prefill_seq_lens,

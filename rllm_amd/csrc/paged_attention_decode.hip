@@ -1801,27 +1801,33 @@ int32_t decode_prefix_impl(void* out, const void* q, const void* kc, const void*
 }
 
 // Mixed batch of one step: the prefill group (chunks of new tokens on their
-// cached context) and the decode group (one token each) over the same cache.
-// With few enough prefill workgroups both run in one mixed_kernel launch: the
-// unsplit prefill workgroups on their own CUs, the stream decode on the
-// others, MIXED_DECODE_WAVES a workgroup for 16-bit caches (one per SIMD:
-// 112.6 us at the step's shape against 118.8 us with two per SIMD) and
+// cached context) and the decode group (one token each) over the same cache,
+// in one mixed_kernel launch: the unsplit prefill workgroups first, then the
+// stream decode's, MIXED_DECODE_WAVES a workgroup for 16-bit caches (one per
+// SIMD: 112.6 us at the step's shape against 118.8 us with two per SIMD) and
 // MIXED_DECODE_WAVES_FP8 for FP8 caches (two per SIMD, as their stream decode
-// runs: a wave converts every byte it reads).  Otherwise the prefill and the
-// decode run in series, as their own entry points do.
+// runs: a wave converts every byte it reads).  Empty groups, shapes outside
+// the tuned set and f16 queries that cannot take the pre-scale run the two
+// entry points in series.
 #ifndef RLLM_MIXED_DECODE_WAVES
 #define RLLM_MIXED_DECODE_WAVES 4
 #endif
 constexpr int64_t MIXED_DECODE_WAVES = RLLM_MIXED_DECODE_WAVES;
 constexpr int64_t MIXED_DECODE_WAVES_FP8 = 8;
-// The prefill group may take at most MIXED_PREFILL_CU_NUM / MIXED_PREFILL_CU_DEN
-// of the CUs; a larger group runs in series (the decode on the CUs left would
-// take longer than the prefill's own launch).  Config 2's decode batch plus one
-// chunk on 2048 cached tokens, step times in one launch against in series:
-// 768 tokens (96 workgroups) 146 against 195 us, 1024 (128) 163 against 189,
-// 1280 (160) 190 against 221, 1536 (192) 246 against 219.
-constexpr int64_t MIXED_PREFILL_CU_NUM = 5;
-constexpr int64_t MIXED_PREFILL_CU_DEN = 8;
+// Where the decode's waves are planned: a prefill group of at most half the
+// CUs' workgroups leaves the decode the other CUs, and the decode's shares are
+// sized for those; a larger group gets the decode planned for the whole GPU,
+// whose workgroups beyond the free CUs start as prefill workgroups finish (a
+// launch's workgroups start in order as CUs free up), so the decode fills the
+// CUs the prefill leaves instead of waiting for a launch of its own.  Config
+// 2's decode batch plus one chunk on 2048 cached tokens, step in us, decode
+// on the free CUs / over the whole GPU / the groups in series:
+//   512 tokens (64 workgroups)   131 / 152 / 164
+//   1024 (128)                   164 / 169 / 191
+//   1280 (160)                   190 / 176 / 221
+//   1536 (192)                   246 / 190 / 219
+//   2048 (256)                     - / 223 / 238
+//   4096 (512)                     - / 366 / 370
 
 int32_t mixed_impl(void* p_out, const void* p_q, const int32_t* p_bt, const int32_t* p_seq_lens,
                    const int32_t* p_qsl, int64_t p_num_seqs, int64_t p_num_tokens, int64_t p_maxb, void* d_out,
@@ -1854,10 +1860,11 @@ int32_t mixed_impl(void* p_out, const void* p_q, const int32_t* p_bt, const int3
     RLLM_CHECK_ARG(pick_kernels(q_dtype, kv_dtype, d, G, &kern));
     const int64_t cus = device_cus();
     const int64_t pw = chunk_base_wgs(p_num_tokens, p_num_seqs, hq, hkv);
-    if (!kern.mixed || cus <= 0 || pw * MIXED_PREFILL_CU_DEN > cus * MIXED_PREFILL_CU_NUM) return serial();
+    if (!kern.mixed || cus <= 0) return serial();
 
-    // the stream decode over the CUs the prefill workgroups leave free
-    const int64_t free_cus = cus - pw;
+    // the stream decode over the CUs the prefill workgroups leave free, or
+    // over the whole GPU past half of them
+    const int64_t free_cus = pw * 2 > cus ? cus : cus - pw;
     const bool fp8 = kv_dtype == KIND_FP8_E4M3 || kv_dtype == KIND_FP8_E5M2;
     const int64_t dpw = fp8 ? MIXED_DECODE_WAVES_FP8 : MIXED_DECODE_WAVES;
     const int max_waves = max_resident_waves();

@@ -155,19 +155,22 @@ def test_mixed_fp8_caches_vs_oracle(dev, fp8):
     assert_close(do, rd, TOL_FP8, f"mixed fp8 decode {fp8}")
 
 
+@pytest.mark.parametrize("nchunks", [3, 8])
 @pytest.mark.parametrize("kv", [O.BF16, O.FP8_E4M3])
-def test_mixed_large_prefill_group_in_series_vs_oracle(dev, kv):
-    """Eight 512-token chunks take more than 5/8 of the CUs (576 workgroups):
-    the groups run in series, the prefill split as its own entry point does."""
-    rng = np.random.default_rng(1601 + kv)
-    c = mixed_case(rng, [512] * 8, [256] * 8, rng.integers(1, 600, size=16), 32, 8, 64)
+def test_mixed_large_prefill_group_vs_oracle(dev, kv, nchunks):
+    """Prefill groups of more than half the CUs' workgroups (three 512-token
+    chunks: 208 workgroups; eight: 576, more than the GPU has CUs): one launch
+    whose decode is planned over the whole GPU, its workgroups starting as
+    prefill workgroups finish."""
+    rng = np.random.default_rng(1601 + kv + 10 * nchunks)
+    c = mixed_case(rng, [512] * nchunks, [256] * nchunks, rng.integers(1, 600, size=16), 32, 8, 64)
     ks = vs = 1.0
     if kv == O.FP8_E4M3:
         ks, vs = float(np.abs(c["k"]).max() / 448.0), float(np.abs(c["v"]).max() / 448.0)
     e = encode(c, O.BF16, kv, ks, vs)
     scale = 0.125
     rp, rd = oracle_ref(e, O.BF16, kv, scale, ks, vs)
-    po, do = run_mixed(dev, e, O.BF16, kv, scale, ks, vs, label="large prefill")
+    po, do = run_mixed(dev, e, O.BF16, kv, scale, ks, vs, label=f"large prefill x{nchunks}")
     tol = TOL_BF16 if kv == O.BF16 else TOL_FP8
     assert_close(po, rp, tol, "mixed large prefill")
     assert_close(do, rd, tol, "mixed large prefill, decode")
