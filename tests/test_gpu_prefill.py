@@ -287,14 +287,16 @@ def test_prefill_fp8_every_byte_converts_exactly(dev, fp8, q_kind):
     assert np.array_equal(got[:, 0, :], want)
 
 
-@pytest.mark.parametrize("shape", [(1, 512, 2048), (4, 256, 4096)])
+@pytest.mark.parametrize("shape", [(1, 512, 2048), (4, 256, 4096), (1, 64, 2048), (1, 128, 4096), (1, 768, 2048)])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("kv", [O.BF16, O.FP8_E4M3, O.FP8_E5M2])
 def test_prefill_kv_split_vs_oracle(dev, shape, D, kv):
     """Small batches split every row's KV range over several workgroups and
-    merge the partials (log-sum-exp) in a second kernel: 1 x 512 new tokens on
-    2048 cached and 4 x 256 on 4096 both take that path.  A merge that drops or
-    mis-weights a split fails the relative-L2 and output-scale bounds."""
+    merge the partials (log-sum-exp) in a second kernel.  On 256 CUs the
+    split counts are 4 (1 x 512 new tokens on 2048 cached), 3 (4 x 256 on
+    4096), 7 (1 x 64 on 2048), 8 (1 x 128 on 4096) and 2 (1 x 768 on 2048).
+    A merge that drops or mis-weights a split fails the relative-L2 and
+    output-scale bounds."""
     nseq, n_new, cached = shape
     rng = np.random.default_rng(1000 + nseq + D + 7 * kv)
     hkv, G = 8, 4
