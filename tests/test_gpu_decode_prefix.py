@@ -256,31 +256,40 @@ def test_prefix_random_sweep_vs_oracle(dev, seed):
     assert_close(got, ref, TOL_BF16 if kv == kind else TOL_FP8, f"prefix sweep {seed}")
 
 
+@pytest.mark.parametrize("kv", [O.BF16, O.FP8_E4M3])
 @pytest.mark.parametrize("B,P,own,cascade", [
     (9, 5, 4, False),      # saves 40 blocks: under the 10,000-tile floor
     (128, 8, 16, False),   # saves 1,016 blocks, under 3/5 of the 2,048 suffix blocks
     (32, 64, 16, True),    # saves 1,984 blocks (15,872 tiles), suffix 512
     (64, 64, 16, True),
 ], ids=["small", "short-prefix", "cascade-32", "cascade-64"])
-def test_prefix_auto_choice_follows_the_rule(dev, monkeypatch, B, P, own, cascade):
+def test_prefix_auto_choice_follows_the_rule(dev, monkeypatch, B, P, own, cascade, kv):
     """Without RLLM_CASCADE the entry point runs the cascade only where the
     prefix saves enough: the cascade when (B - 1) * P >= 3/5 * B * own and
     (B - 1) * P * Hkv >= 10,000, else the plain decode.  Its output has the
     forced cascade's bits or the plain decode's, as the rule says, and
     RLLM_CASCADE=never gives the plain decode's."""
-    rng = np.random.default_rng(4100 + B + P)
+    rng = np.random.default_rng(4100 + B + P + kv)
     q, k, v, bt, sl = prefix_case(rng, B, 32, 8, 128, P, (own * 16, own * 16))
     assert bt.shape[1] == P + own
-    qb, kb, vb = O.encode(q, O.BF16), O.encode(k, O.BF16), O.encode(v, O.BF16)
+    qb = O.encode(q, O.BF16)
+    ks = vs = 1.0
+    if kv == O.FP8_E4M3:
+        ks, vs = float(np.abs(k).max() / 448.0), float(np.abs(v).max() / 448.0)
+        kb = O.encode((k / np.float32(ks)).astype(np.float32), kv)
+        vb = O.encode((v / np.float32(vs)).astype(np.float32), kv)
+    else:
+        kb, vb = O.encode(k, kv), O.encode(v, kv)
     scale = 1 / np.sqrt(128)
-    forced = run_prefix(dev, qb, O.BF16, kb, vb, O.BF16, bt, sl, scale, P, label=f"forced B={B}")
+    args = (dev, qb, O.BF16, kb, vb, kv, bt, sl, scale, P, ks, vs)
+    forced = run_prefix(*args, label=f"forced B={B}")
     monkeypatch.delenv("RLLM_CASCADE")
-    auto = run_prefix(dev, qb, O.BF16, kb, vb, O.BF16, bt, sl, scale, P, label=f"auto B={B}")
+    auto = run_prefix(*args, label=f"auto B={B}")
     monkeypatch.setenv("RLLM_CASCADE", "never")
-    never = run_prefix(dev, qb, O.BF16, kb, vb, O.BF16, bt, sl, scale, P, label=f"never B={B}")
-    plain = f32(ops.paged_decode(t16(qb, torch.bfloat16, dev), t16(kb, torch.bfloat16, dev),
-                                 t16(vb, torch.bfloat16, dev), ti(bt, torch.int32, dev), ti(sl, torch.int32, dev),
-                                 scale))
+    never = run_prefix(*args, label=f"never B={B}")
+    plain = f32(ops.paged_decode(t16(qb, torch.bfloat16, dev), _kv(kb, kv, dev), _kv(vb, kv, dev),
+                                 ti(bt, torch.int32, dev), ti(sl, torch.int32, dev), scale, kv_dtype=ABI[kv],
+                                 k_scale=ks, v_scale=vs))
     assert np.array_equal(never, plain)
     assert np.array_equal(auto, forced if cascade else plain)
     assert np.max(np.abs(forced - plain)) <= 2 ** -7 * max(1.0, float(np.abs(plain).max()))

@@ -176,6 +176,26 @@ def test_mixed_large_prefill_group_vs_oracle(dev, kv, nchunks):
     assert_close(do, rd, tol, "mixed large prefill, decode")
 
 
+@pytest.mark.parametrize("q_kind,kv", [(O.F16, O.F16), (O.F16, O.FP8_E5M2), (O.BF16, O.FP8_E5M2)],
+                         ids=["f16", "f16-e5m2", "bf16-e5m2"])
+def test_mixed_large_prefill_group_other_types_vs_oracle(dev, q_kind, kv):
+    """The whole-GPU decode plan with f16 queries and caches and E5M2 caches:
+    four 384-token chunks (216 workgroups by the grid's bound at head_dim 128,
+    GQA 4) beside 24 decode sequences."""
+    rng = np.random.default_rng(1701 + 3 * q_kind + kv)
+    c = mixed_case(rng, [384] * 4, [700, 0, 1300, 64], rng.integers(1, 2500, size=24), 32, 8, 128)
+    ks = vs = 1.0
+    if kv == O.FP8_E5M2:
+        ks, vs = float(np.abs(c["k"]).max() / 57344.0), float(np.abs(c["v"]).max() / 57344.0)
+    e = encode(c, q_kind, kv, ks, vs)
+    scale = 1 / np.sqrt(128)
+    rp, rd = oracle_ref(e, q_kind, kv, scale, ks, vs)
+    po, do = run_mixed(dev, e, q_kind, kv, scale, ks, vs, label="large prefill, other types")
+    tol = TOL_BF16 if kv == q_kind else TOL_FP8
+    assert_close(po, rp, tol, "mixed large prefill, other types")
+    assert_close(do, rd, tol, "mixed large prefill, other types, decode")
+
+
 def test_mixed_one_wave_decode_and_empty_groups(dev):
     """A decode group of one short sequence (a single stream wave, no
     workspace); a step without decode tokens and one without prefill tokens
